@@ -1,0 +1,398 @@
+// fna2_capi.cpp — the extern "C" boundary: validation, workspace layout and
+// kernel dispatch.  Host code only; every GPU launch goes through the
+// launch_* wrappers of the .hip files.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <mutex>
+
+#include "fna2.h"
+#include "fna2_kernels.h"
+#include "fna2_sched.h"
+
+namespace {
+
+using fna2::kDqBM;
+using fna2::kDqBN;
+using fna2::kFwdBM;
+using fna2::kFwdBN;
+using fna2::kKvBM;
+using fna2::kKvBN;
+
+constexpr size_t kAlign = 256;
+constexpr int64_t kMaxGrid = (int64_t)1 << 24;  // workgroups per launch
+
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+int64_t cdiv64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Rows of the query / key side (dense: B * S, varlen: tokens).
+int64_t rows_q(const fna2_problem& p) {
+  return p.varlen ? (int64_t)p.total_q : (int64_t)p.batch * p.seqlen_q;
+}
+int64_t rows_k(const fna2_problem& p) {
+  return p.varlen ? (int64_t)p.total_k : (int64_t)p.batch * p.seqlen_k;
+}
+
+int check_problem(const fna2_problem& p) {
+  if (p.dtype != FNA2_BF16) return FNA2_E_DTYPE;
+  if (p.head_dim != 64 && p.head_dim != 128) return FNA2_E_HEAD_DIM;
+  if (p.heads <= 0 || p.heads_kv <= 0 || p.heads % p.heads_kv != 0) return FNA2_E_HEADS;
+  if (p.heads_graph < 0 || p.heads_graph > p.heads) return FNA2_E_HEADS;
+  if (p.heads_graph > 0 && (p.rank < 8 || p.rank > 64 || p.rank % 8 != 0)) return FNA2_E_RANK;
+  if (p.batch < 0) return FNA2_E_SHAPE;
+  if (p.varlen) {
+    if (p.total_q < 0 || p.total_k < 0) return FNA2_E_SHAPE;
+    if (p.batch > 0 && (!p.cu_seqlens_q || !p.cu_seqlens_k)) return FNA2_E_SEQLENS;
+  } else {
+    if (p.seqlen_q < 0 || p.seqlen_k < 0) return FNA2_E_SHAPE;
+  }
+  if (!std::isfinite(p.softmax_scale)) return FNA2_E_SCALE;
+  return FNA2_OK;
+}
+
+// feat: elements per row (16-byte vectors) or 0 for an fp32 scalar view.
+int check_view(const fna2_tensor& t, const fna2_problem& p, bool required, bool vec,
+               size_t esize) {
+  if (!required) return FNA2_OK;
+  if (!t.ptr) return FNA2_E_NULL;
+  const size_t a = vec ? 16 : esize;
+  if (!aligned(t.ptr, a)) return FNA2_E_STRIDE;
+  const int64_t ss = t.stride_s, sh = t.stride_h, sb = p.varlen ? 0 : t.stride_b;
+  const int64_t unit = vec ? (int64_t)(16 / esize) : 1;
+  if (ss % unit || sh % unit || sb % unit) return FNA2_E_STRIDE;
+  return FNA2_OK;
+}
+
+#define FNA2_TRY(x)              \
+  do {                           \
+    int _s = (x);                \
+    if (_s != FNA2_OK) return _s; \
+  } while (0)
+
+struct Grids {
+  int64_t fwd_bound = 0;  // varlen tile-list capacity
+  int64_t fwd_grid = 0;
+  int64_t dq_bound = 0, dq_grid = 0;
+  int64_t kv_bound = 0, kv_grid = 0;
+};
+
+Grids grids(const fna2_problem& p) {
+  Grids g;
+  if (p.batch <= 0) return g;
+  if (p.varlen) {
+    g.fwd_bound = fna2::tile_bound(p.total_q, p.batch, kFwdBM);
+    g.fwd_grid = g.fwd_bound * p.heads;
+    g.dq_bound = fna2::tile_bound(p.total_q, p.batch, kDqBM);
+    g.dq_grid = g.dq_bound * p.heads;
+    g.kv_bound = fna2::tile_bound(p.total_k, p.batch, kKvBN);
+    g.kv_grid = g.kv_bound * p.heads_kv;
+  } else {
+    g.fwd_grid = (int64_t)p.batch * cdiv64(p.seqlen_q, kFwdBM) * p.heads;
+    g.dq_grid = (int64_t)p.batch * cdiv64(p.seqlen_q, kDqBM) * p.heads;
+    g.kv_grid = (int64_t)p.batch * cdiv64(p.seqlen_k, kKvBN) * p.heads_kv;
+  }
+  return g;
+}
+
+int check_grids(const fna2_problem& p) {
+  const Grids g = grids(p);
+  if (g.fwd_grid > kMaxGrid || g.dq_grid > kMaxGrid || g.kv_grid > kMaxGrid) return FNA2_E_SHAPE;
+  const int64_t dthreads = rows_q(p) * p.heads * (p.head_dim / 8);
+  if (cdiv64(dthreads, 256) > kMaxGrid) return FNA2_E_SHAPE;
+  if (rows_q(p) > INT32_MAX || rows_k(p) > INT32_MAX) return FNA2_E_SHAPE;
+  return FNA2_OK;
+}
+
+// Workspace layouts (byte offsets), all 256-byte aligned.
+struct FwdWs {
+  size_t tiles = 0, count = 0, bytes = 0;
+};
+FwdWs fwd_ws(const fna2_problem& p) {
+  FwdWs w;
+  const Grids g = grids(p);
+  if (p.varlen && g.fwd_bound > 0) {
+    w.tiles = 0;
+    w.count = align_up(sizeof(int2) * g.fwd_bound);
+    w.bytes = w.count + kAlign;
+  }
+  return w;
+}
+
+struct BwdWs {
+  size_t tiles_q = 0, count_q = 0, tiles_k = 0, count_k = 0, partial = 0, bytes = 0;
+};
+BwdWs bwd_ws(const fna2_problem& p) {
+  BwdWs w;
+  const Grids g = grids(p);
+  size_t off = 0;
+  if (p.varlen && g.dq_bound > 0) {
+    w.tiles_q = off;
+    off += align_up(sizeof(int2) * g.dq_bound);
+    w.count_q = off;
+    off += kAlign;
+    w.tiles_k = off;
+    off += align_up(sizeof(int2) * g.kv_bound);
+    w.count_k = off;
+    off += kAlign;
+  }
+  w.partial = off;
+  off += align_up(sizeof(float) * (size_t)(g.dq_grid > 0 ? g.dq_grid : 1));
+  w.bytes = off;
+  return w;
+}
+
+fna2::Problem make_problem(const fna2_problem& p) {
+  fna2::Problem P;
+  std::memset(&P, 0, sizeof(P));
+  P.varlen = p.varlen;
+  P.nseq = p.batch;
+  P.sq = p.varlen ? 0 : p.seqlen_q;
+  P.sk = p.varlen ? 0 : p.seqlen_k;
+  P.total_q = p.varlen ? p.total_q : 0;
+  P.total_k = p.varlen ? p.total_k : 0;
+  P.H = p.heads;
+  P.H_KV = p.heads_kv;
+  P.H_G = p.heads_graph;
+  P.D = p.head_dim;
+  P.R = p.heads_graph > 0 ? p.rank : 0;
+  P.causal = p.causal ? 1 : 0;
+  P.group = p.heads / p.heads_kv;
+  const float s = p.softmax_scale;
+  if (s > 0.f) {
+    P.c = s;
+    P.qa = 1.f;
+  } else if (s < 0.f) {
+    P.c = -s;
+    P.qa = -1.f;
+  } else {
+    P.c = 1.f;
+    P.qa = 0.f;
+  }
+  P.c2 = P.c * fna2::kLog2e;
+  P.cu_q = p.cu_seqlens_q;
+  P.cu_k = p.cu_seqlens_k;
+  return P;
+}
+
+// Records caller-owned event i on the stream when events are requested.
+bool mark(void* const* events, int i, hipStream_t stream) {
+  if (!events || !events[i]) return true;
+  return hipEventRecord((hipEvent_t)events[i], stream) == hipSuccess;
+}
+
+fna2::TView view(const fna2_tensor& t) {
+  fna2::TView v;
+  v.ptr = t.ptr;
+  v.sb = t.stride_b;
+  v.ss = t.stride_s;
+  v.sh = t.stride_h;
+  return v;
+}
+
+int max_iters(const fna2_problem& p, int hint, int total, int step) {
+  int64_t n = hint > 0 ? hint : total;
+  return (int)std::min<int64_t>(cdiv64(n, step), 1 << 20);
+}
+
+// Kernels exist for gfx950 only; cache the answer per device.
+int check_device() {
+  static std::mutex mu;
+  static int state[64] = {0};  // 0 unknown, 1 ok, -1 wrong arch
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return FNA2_E_DEVICE;
+  if (dev < 0 || dev >= 64) return FNA2_E_DEVICE;
+  std::lock_guard<std::mutex> lk(mu);
+  if (state[dev] == 0) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return FNA2_E_DEVICE;
+    state[dev] = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
+  }
+  return state[dev] == 1 ? FNA2_OK : FNA2_E_DEVICE;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fna2_version(void) { return FNA2_ABI_VERSION; }
+
+const char* fna2_status_string(int s) {
+  switch (s) {
+    case FNA2_OK: return "ok";
+    case FNA2_E_NULL: return "a required pointer is NULL";
+    case FNA2_E_DTYPE: return "unsupported dtype (bf16 only)";
+    case FNA2_E_HEAD_DIM: return "head_dim must be 64 or 128";
+    case FNA2_E_RANK: return "rank must be a multiple of 8 in [8, 64]";
+    case FNA2_E_HEADS: return "heads must be a multiple of heads_kv and heads_graph <= heads";
+    case FNA2_E_SHAPE: return "negative extent or problem too large";
+    case FNA2_E_STRIDE: return "pointer or stride breaks 16-byte row alignment";
+    case FNA2_E_SEQLENS: return "varlen mode needs cu_seqlens_q and cu_seqlens_k";
+    case FNA2_E_WORKSPACE: return "workspace missing or too small";
+    case FNA2_E_LAUNCH: return "kernel launch failed";
+    case FNA2_E_DEVICE: return "current device is not gfx950";
+    case FNA2_E_SCALE: return "softmax_scale must be finite";
+  }
+  return "unknown status";
+}
+
+int fna2_check_fwd(const fna2_fwd_args* a) {
+  if (!a) return FNA2_E_NULL;
+  const fna2_problem& p = a->p;
+  FNA2_TRY(check_problem(p));
+  FNA2_TRY(check_grids(p));
+  const bool qw = rows_q(p) > 0, kw = rows_k(p) > 0;
+  const bool g = p.heads_graph > 0;
+  FNA2_TRY(check_view(a->q, p, qw, true, 2));
+  FNA2_TRY(check_view(a->out, p, qw, true, 2));
+  FNA2_TRY(check_view(a->lse, p, qw, false, 4));
+  FNA2_TRY(check_view(a->k, p, qw && kw, true, 2));
+  FNA2_TRY(check_view(a->v, p, qw && kw, true, 2));
+  FNA2_TRY(check_view(a->r_q, p, qw && g, true, 2));
+  FNA2_TRY(check_view(a->r_k, p, qw && kw && g, true, 2));
+  if (qw && g && !a->graph_scale) return FNA2_E_NULL;
+  if (a->workspace_bytes < fwd_ws(p).bytes || (fwd_ws(p).bytes && !a->workspace))
+    return FNA2_E_WORKSPACE;
+  return FNA2_OK;
+}
+
+int fna2_check_bwd(const fna2_bwd_args* a) {
+  if (!a) return FNA2_E_NULL;
+  const fna2_problem& p = a->p;
+  FNA2_TRY(check_problem(p));
+  FNA2_TRY(check_grids(p));
+  const bool qw = rows_q(p) > 0, kw = rows_k(p) > 0;
+  const bool g = p.heads_graph > 0;
+  FNA2_TRY(check_view(a->q, p, qw, true, 2));
+  FNA2_TRY(check_view(a->out, p, qw, true, 2));
+  FNA2_TRY(check_view(a->dout, p, qw, true, 2));
+  FNA2_TRY(check_view(a->dq, p, qw, true, 2));
+  FNA2_TRY(check_view(a->lse, p, qw, false, 4));
+  FNA2_TRY(check_view(a->delta, p, qw, false, 4));
+  FNA2_TRY(check_view(a->k, p, kw, true, 2));
+  FNA2_TRY(check_view(a->v, p, kw, true, 2));
+  FNA2_TRY(check_view(a->dk, p, kw, true, 2));
+  FNA2_TRY(check_view(a->dv, p, kw, true, 2));
+  FNA2_TRY(check_view(a->r_q, p, qw && g, true, 2));
+  FNA2_TRY(check_view(a->dr_q, p, qw && g, true, 2));
+  FNA2_TRY(check_view(a->r_k, p, kw && g, true, 2));
+  FNA2_TRY(check_view(a->dr_k, p, kw && g, true, 2));
+  if (g && (!a->graph_scale || !a->d_graph_scale)) return FNA2_E_NULL;
+  const BwdWs w = bwd_ws(p);
+  if (a->workspace_bytes < w.bytes || !a->workspace) return FNA2_E_WORKSPACE;
+  return FNA2_OK;
+}
+
+size_t fna2_fwd_workspace_bytes(const fna2_problem* p) {
+  if (!p || check_problem(*p) != FNA2_OK) return 0;
+  return fwd_ws(*p).bytes;
+}
+
+size_t fna2_bwd_workspace_bytes(const fna2_problem* p) {
+  if (!p || check_problem(*p) != FNA2_OK) return 0;
+  return bwd_ws(*p).bytes;
+}
+
+int fna2_fwd(const fna2_fwd_args* a, void* stream_ptr) {
+  FNA2_TRY(fna2_check_fwd(a));
+  const fna2_problem& p = a->p;
+  if (rows_q(p) == 0 || p.batch == 0) return FNA2_OK;
+  FNA2_TRY(check_device());
+  hipStream_t stream = (hipStream_t)stream_ptr;
+  fna2::FwdParams K;
+  std::memset(&K, 0, sizeof(K));
+  K.p = make_problem(p);
+  K.q = view(a->q);
+  K.k = view(a->k);
+  K.v = view(a->v);
+  K.rq = view(a->r_q);
+  K.rk = view(a->r_k);
+  K.o = view(a->out);
+  K.lse = view(a->lse);
+  K.gs = a->graph_scale;
+  const Grids g = grids(p);
+  if (p.varlen) {
+    const FwdWs w = fwd_ws(p);
+    int2* tiles = (int2*)((char*)a->workspace + w.tiles);
+    int* count = (int*)((char*)a->workspace + w.count);
+    fna2::TileSpec spec{0, kFwdBM, kFwdBN};
+    if (fna2::launch_build_tiles(K.p, spec, max_iters(p, p.seqlen_k, p.total_k, kFwdBN), tiles,
+                                 count, (int)g.fwd_bound, stream) != hipSuccess)
+      return FNA2_E_LAUNCH;
+    K.tiles = tiles;
+    K.n_tiles = count;
+  }
+  const int rp = fna2::padded_rank(K.p.H_G, K.p.R);
+  if (!mark(a->events, 0, stream)) return FNA2_E_LAUNCH;
+  if (fna2::launch_fwd(K, rp, (int)g.fwd_grid, stream) != hipSuccess) return FNA2_E_LAUNCH;
+  if (!mark(a->events, 1, stream)) return FNA2_E_LAUNCH;
+  return FNA2_OK;
+}
+
+int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
+  FNA2_TRY(fna2_check_bwd(a));
+  const fna2_problem& p = a->p;
+  FNA2_TRY(check_device());
+  hipStream_t stream = (hipStream_t)stream_ptr;
+  fna2::BwdParams K;
+  std::memset(&K, 0, sizeof(K));
+  K.p = make_problem(p);
+  K.q = view(a->q);
+  K.k = view(a->k);
+  K.v = view(a->v);
+  K.rq = view(a->r_q);
+  K.rk = view(a->r_k);
+  K.o = view(a->out);
+  K.lse = view(a->lse);
+  K.dout = view(a->dout);
+  K.delta = view(a->delta);
+  K.dq = view(a->dq);
+  K.dk = view(a->dk);
+  K.dv = view(a->dv);
+  K.drq = view(a->dr_q);
+  K.drk = view(a->dr_k);
+  K.gs = a->graph_scale;
+  K.dgs = a->d_graph_scale;
+  const BwdWs w = bwd_ws(p);
+  const Grids g = grids(p);
+  K.dgs_partial = (float*)((char*)a->workspace + w.partial);
+  const int rp = fna2::padded_rank(K.p.H_G, K.p.R);
+
+  if (p.batch > 0 && (rows_q(p) > 0 || rows_k(p) > 0)) {
+    if (!mark(a->events, 0, stream)) return FNA2_E_LAUNCH;
+    if (fna2::launch_bwd_delta(K, stream) != hipSuccess) return FNA2_E_LAUNCH;
+    if (!mark(a->events, 1, stream)) return FNA2_E_LAUNCH;
+    if (p.varlen) {
+      int2* tq = (int2*)((char*)a->workspace + w.tiles_q);
+      int* cq = (int*)((char*)a->workspace + w.count_q);
+      int2* tk = (int2*)((char*)a->workspace + w.tiles_k);
+      int* ck = (int*)((char*)a->workspace + w.count_k);
+      fna2::TileSpec sq{0, kDqBM, kDqBN};
+      fna2::TileSpec sk{1, kKvBN, kKvBM};
+      if (fna2::launch_build_tiles(K.p, sq, max_iters(p, p.seqlen_k, p.total_k, kDqBN), tq, cq,
+                                   (int)g.dq_bound, stream) != hipSuccess)
+        return FNA2_E_LAUNCH;
+      if (fna2::launch_build_tiles(K.p, sk, max_iters(p, p.seqlen_q, p.total_q, kKvBM), tk, ck,
+                                   (int)g.kv_bound, stream) != hipSuccess)
+        return FNA2_E_LAUNCH;
+      K.tiles_q = tq;
+      K.n_tiles_q = cq;
+      K.tiles_k = tk;
+      K.n_tiles_k = ck;
+    }
+    if (!mark(a->events, 2, stream)) return FNA2_E_LAUNCH;
+    if (rows_k(p) > 0 && fna2::launch_bwd_dkdv(K, rp, (int)g.kv_grid, stream) != hipSuccess)
+      return FNA2_E_LAUNCH;
+    if (!mark(a->events, 3, stream) || !mark(a->events, 4, stream)) return FNA2_E_LAUNCH;
+    if (rows_q(p) > 0 && fna2::launch_bwd_dq(K, rp, (int)g.dq_grid, stream) != hipSuccess)
+      return FNA2_E_LAUNCH;
+    if (!mark(a->events, 5, stream)) return FNA2_E_LAUNCH;
+  }
+  if (fna2::launch_bwd_dgs(K, (int)g.dq_grid, stream) != hipSuccess) return FNA2_E_LAUNCH;
+  return FNA2_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,154 @@
+// fna2_device.h — device-side types and helpers shared by the gfx950 kernels.
+//
+// Conventions used by every kernel in this directory:
+//  * bf16 tensors are addressed as uint16_t; strides are in elements.
+//  * The augmented contraction: for query head h the kernels multiply
+//        Qa_i = [ a * Q_i | b_h * Rq_i ]   with   Ka_j = [ K_j | Rk_j ]
+//    so that S_ij = c * <Qa_i, Ka_j>.  The host picks c > 0 and a in {1,-1,0}
+//    with c * a = softmax_scale; b_h = graph_scale[h] / c.  The Q part is
+//    therefore never rounded, only the bias operand b_h * Rq is (once, to bf16).
+//  * MFMA: v_mfma_f32_32x32x16_bf16.  Operand lane layout (A rows / B columns
+//    on lane % 32, the 8 k-values of a 16-deep step on lane / 32) and the
+//    accumulator layout (column = lane % 32, row = 8*(v/4) + 4*(lane/32) + v%4
+//    for accumulator register v) are the CDNA 32x32 layouts.  A 16-deep step
+//    built from accumulator registers 8s..8s+7 therefore holds rows
+//    16s + perm16(8*(lane/32) + e), e = 0..7, with perm16 below; operands that
+//    are read from LDS to meet such a register operand store their 16-row
+//    groups in that permuted order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fna2 {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_inff();
+
+// One tensor view: base + element strides (batch, sequence/token, head).
+struct TView {
+  const void* ptr;
+  int64_t sb, ss, sh;
+};
+
+// Everything a kernel needs to know about the problem, passed by value.
+struct Problem {
+  int varlen;
+  int nseq;        // dense B or varlen N
+  int sq, sk;      // dense lengths (varlen: unused)
+  int total_q, total_k;
+  int H, H_KV, H_G, D, R;
+  int causal;
+  int group;       // H / H_KV
+  float c;         // positive score multiplier
+  float c2;        // c * log2(e)
+  float qa;        // a in {1, -1, 0}
+  const int* cu_q;
+  const int* cu_k;
+};
+
+// Sequence extents, clamped so that no access leaves [0, total).
+struct SeqExt {
+  int q0, lq, k0, lk;
+};
+
+__device__ __forceinline__ SeqExt seq_ext(const Problem& p, int b) {
+  SeqExt e;
+  if (p.varlen) {
+    int qs = p.cu_q[b], qe = p.cu_q[b + 1];
+    int ks = p.cu_k[b], ke = p.cu_k[b + 1];
+    qs = min(max(qs, 0), p.total_q);
+    qe = min(max(qe, qs), p.total_q);
+    ks = min(max(ks, 0), p.total_k);
+    ke = min(max(ke, ks), p.total_k);
+    e.q0 = qs; e.lq = qe - qs; e.k0 = ks; e.lk = ke - ks;
+  } else {
+    e.q0 = 0; e.lq = p.sq; e.k0 = 0; e.lk = p.sk;
+  }
+  return e;
+}
+
+// Base pointer of sequence b, head h of a view; row r is at base + r * ss.
+template <typename T>
+__device__ __forceinline__ T* seq_base(const TView& t, const Problem& p, int b,
+                                       int start, int h) {
+  int64_t off = p.varlen ? (int64_t)start * t.ss : (int64_t)b * t.sb;
+  return (T*)t.ptr + off + (int64_t)h * t.sh;
+}
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+  return *(const u32x4*)p;
+}
+
+__device__ __forceinline__ void st16(void* p, u32x4 v) { *(u32x4*)p = v; }
+
+// Round two floats to bf16 (RNE) and pack: lo in bits 0..15.
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  f32x2 x = {lo, hi};
+  bf16x2 y = __builtin_convertvector(x, bf16x2);
+  return __builtin_bit_cast(uint32_t, y);
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) {
+  return __builtin_bit_cast(float, w << 16);
+}
+__device__ __forceinline__ float bf16_hi(uint32_t w) {
+  return __builtin_bit_cast(float, w & 0xffff0000u);
+}
+
+// Eight bf16 values times s, rounded back to bf16.
+__device__ __forceinline__ u32x4 scale_bf16x8(u32x4 v, float s) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = pack_bf16(bf16_lo(v[i]) * s, bf16_hi(v[i]) * s);
+  return r;
+}
+
+// Position of row k (0..15) inside a permuted 16-row group (see header).
+__device__ __forceinline__ int perm16(int k) {
+  return (k & 3) | (((k >> 3) & 1) << 2) | (((k >> 2) & 1) << 3);
+}
+
+// Transpose helper: element e (0..7) of four 16-byte rows r0..r3, packed as
+// four bf16 (row order) into 8 bytes.
+__device__ __forceinline__ u32x2 gather4(const u32x4& r0, const u32x4& r1,
+                                         const u32x4& r2, const u32x4& r3, int e) {
+  const int w = e >> 1;
+  u32x2 out;
+  if (e & 1) {
+    out[0] = (r0[w] >> 16) | (r1[w] & 0xffff0000u);
+    out[1] = (r2[w] >> 16) | (r3[w] & 0xffff0000u);
+  } else {
+    out[0] = (r0[w] & 0xffffu) | (r1[w] << 16);
+    out[1] = (r2[w] & 0xffffu) | (r3[w] << 16);
+  }
+  return out;
+}
+
+__device__ __forceinline__ float wave_pair_max(float x) {
+  return fmaxf(x, __shfl_xor(x, 32));
+}
+__device__ __forceinline__ float wave_pair_sum(float x) {
+  return x + __shfl_xor(x, 32);
+}
+
+__device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+}  // namespace fna2

@@ -1,0 +1,50 @@
+// fna2_kernels.h — kernel parameter blocks and host launch wrappers.
+#pragma once
+
+#include "fna2_device.h"
+
+namespace fna2 {
+
+struct FwdParams {
+  Problem p;
+  TView q, k, v, rq, rk, o, lse;
+  const float* gs;
+  const int2* tiles;   // varlen: device tile list (null in dense mode)
+  const int* n_tiles;  // varlen: device tile count
+};
+
+struct BwdParams {
+  Problem p;
+  TView q, k, v, rq, rk, o, lse, dout, delta, dq, dk, dv, drq, drk;
+  const float* gs;
+  float* dgs;            // [H_G]
+  float* dgs_partial;    // [dq grid] per-workgroup partial sums of d_gs
+  const int2* tiles_q;   // varlen: query tiles (dQ kernel)
+  const int* n_tiles_q;
+  const int2* tiles_k;   // varlen: key tiles (dK/dV kernel)
+  const int* n_tiles_k;
+};
+
+// Forward tile shape (queries per workgroup / keys per iteration).
+constexpr int kFwdBM = 128;
+constexpr int kFwdBN = 64;
+// Backward: dK/dV kernel tiles keys by kKvBN and walks queries kKvBM at a
+// time; the dQ kernel tiles queries by kDqBM and walks keys kDqBN at a time.
+constexpr int kKvBN = 128;
+constexpr int kKvBM = 32;
+constexpr int kDqBM = 128;
+constexpr int kDqBN = 32;
+
+// Padded rank used by the kernels: 0 without graph heads, else R rounded up
+// to a multiple of 16.
+inline int padded_rank(int H_G, int R) {
+  return (H_G > 0 && R > 0) ? ((R + 15) / 16) * 16 : 0;
+}
+
+hipError_t launch_fwd(const FwdParams& P, int rp, int grid, hipStream_t s);
+hipError_t launch_bwd_delta(const BwdParams& P, hipStream_t s);
+hipError_t launch_bwd_dkdv(const BwdParams& P, int rp, int grid, hipStream_t s);
+hipError_t launch_bwd_dq(const BwdParams& P, int rp, int grid, hipStream_t s);
+hipError_t launch_bwd_dgs(const BwdParams& P, int nparts, hipStream_t s);
+
+}  // namespace fna2

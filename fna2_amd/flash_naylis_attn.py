@@ -1,0 +1,469 @@
+"""FlashNaylisAttention-2 on MI355X: the drop-in for ``FNA2/flash_naylis_attn.py``.
+
+Same public surface as the reference module (myAiByMe/FNA2,
+``FNA2/flash_naylis_attn.py``):
+
+* ``BLOCK_M``, ``BLOCK_N``, ``BLOCK_R`` (:49-51) — ``BLOCK_R`` still names the
+  default rank that ``NaylisAttention`` checks (attention_fna2.py:225);
+* the launchers ``_fna2_forward`` (:700), ``_fna2_forward_varlen`` (:756),
+  ``_fna2_backward`` (:807), ``_fna2_backward_varlen`` (:1215);
+* ``FlashNaylisAttnFunc`` (:1307, 12 inputs, 12 gradients);
+* ``flash_naylis_attn`` (:1380).
+
+The launchers call hand-written gfx950 HIP kernels through the C ABI of
+``include/fna2.h`` (``libfna2_hip.so``, bound with ctypes in ``_capi.py``).
+There is no Triton and no fallback path: without the library every call
+raises.
+
+Differences from the reference, all supersets:
+
+* rank ``R`` may be any multiple of 8 in [8, 64] (the reference requires
+  ``R == BLOCK_R == 32``, :719, :778, :1423-1427);
+* varlen honours ``is_causal`` (the reference's varlen kernels are always
+  causal, :300, :322) — ``_fna2_forward_varlen`` / ``_fna2_backward_varlen``
+  take it as an extra trailing keyword that defaults to ``True``;
+* ``S_q != S_k`` in dense mode and ``cu_seqlens_q != cu_seqlens_k`` in varlen
+  mode (top-left causal alignment, as the reference's masks);
+* ``r_q=None`` runs plain attention (no graph heads);
+* gradients are exact sums (the reference accumulates dK/dV/dR_k with bf16
+  atomics, :546-553) and bitwise reproducible.
+
+Tensors need a unit innermost stride and 16-byte aligned rows; other layouts
+are copied with ``.contiguous()`` first.  Inputs must be bfloat16.
+"""
+from __future__ import annotations
+
+import contextlib
+import ctypes
+import math
+from typing import Optional
+
+import torch
+
+from . import _capi
+
+BLOCK_M = 128  # query rows per forward workgroup
+BLOCK_N = 64   # keys per forward step
+BLOCK_R = 32   # default rel_rank (NaylisAttention's default)
+
+SUPPORTED_HEAD_DIMS = (64, 128)
+SUPPORTED_RANKS = tuple(range(8, 65, 8))
+
+
+def rank_supported(r: int) -> bool:
+    return r in SUPPORTED_RANKS
+
+
+# ─────────────────────────────────────────────────────────────────────────────
+# tensor views for the C ABI
+# ─────────────────────────────────────────────────────────────────────────────
+
+def _aligned(t: torch.Tensor, vec: bool) -> bool:
+    if t.stride(-1) != 1 and t.shape[-1] > 1:
+        return False
+    es = t.element_size()
+    unit = 16 // es if vec else 1
+    if vec and t.data_ptr() % 16:
+        return False
+    return all(s % unit == 0 for s in t.stride()[:-1])
+
+
+def _prep(t: Optional[torch.Tensor], vec: bool = True) -> Optional[torch.Tensor]:
+    if t is None:
+        return None
+    if t.numel() == 0:
+        return t
+    if not _aligned(t, vec):
+        t = t.contiguous()
+    return t
+
+
+def _view4(t: Optional[torch.Tensor]) -> _capi.Tensor:
+    """Dense [B, H, S, F] (or fp32 [B, H, S])."""
+    if t is None or t.numel() == 0:
+        return _capi.empty_tensor()
+    return _capi.Tensor(t.data_ptr(), t.stride(0), t.stride(2), t.stride(1))
+
+
+def _view3(t: Optional[torch.Tensor]) -> _capi.Tensor:
+    """Varlen [T, H, F] (or fp32 [T, H])."""
+    if t is None or t.numel() == 0:
+        return _capi.empty_tensor()
+    return _capi.Tensor(t.data_ptr(), 0, t.stride(0), t.stride(1))
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None or t.numel() == 0 else t.data_ptr()
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _check_inputs(q, k, v, r_q, r_k, graph_scale):
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        assert t.dtype == torch.bfloat16, f"{name} must be bfloat16 (got {t.dtype})"
+        assert t.is_cuda, f"{name} must be a GPU tensor"
+    if r_q is not None:
+        assert r_k is not None, "r_q and r_k must both be given"
+        assert r_q.dtype == torch.bfloat16 and r_k.dtype == torch.bfloat16, \
+            "r_q and r_k must be bfloat16"
+        assert graph_scale is not None, "graph_scale is required with r_q / r_k"
+    dev = q.device
+    for t in (k, v, r_q, r_k, graph_scale):
+        if t is not None:
+            assert t.device == dev, "all tensors must be on the same device"
+
+
+def _gs32(graph_scale: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    if graph_scale is None:
+        return None
+    return graph_scale.detach().to(torch.float32).contiguous()
+
+
+def _problem(varlen, batch, sq, sk, tq, tk, H, H_KV, H_G, D, R, causal, scale, cu_q=None,
+             cu_k=None) -> _capi.Problem:
+    return _capi.Problem(_capi.FNA2_BF16, int(varlen), int(batch), int(sq), int(sk), int(tq),
+                         int(tk), int(H), int(H_KV), int(H_G), int(D), int(R), int(bool(causal)),
+                         float(scale), _ptr(cu_q), _ptr(cu_k))
+
+
+class KernelTimer:
+    """Per-kernel HIP event pairs, recorded by the library around its kernels.
+
+    Used by ``bench.py`` through :func:`kernel_timing`.  Events come from a
+    pool created (and materialised by one record) before the timed region, so
+    timing adds only the event records themselves to the stream.
+    """
+
+    FWD = ("fwd",)
+    BWD = ("delta", "dkdv", "dq")
+
+    def __init__(self, n_fwd: int, n_bwd: int):
+        n = 2 * (n_fwd * len(self.FWD) + n_bwd * len(self.BWD))
+        self._pool = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+        for ev in self._pool:
+            ev.record()
+        torch.cuda.synchronize()
+        self._next = 0
+        self.records = []  # (kernel name, start event, end event)
+
+    def take(self, names) -> ctypes.Array:
+        evs = []
+        for name in names:
+            if self._next + 2 > len(self._pool):
+                raise RuntimeError("KernelTimer pool exhausted")
+            s, e = self._pool[self._next], self._pool[self._next + 1]
+            self._next += 2
+            self.records.append((name, s, e))
+            evs += [s, e]
+        return (ctypes.c_void_p * len(evs))(*[ev.cuda_event for ev in evs])
+
+    def durations_ms(self) -> dict:
+        torch.cuda.synchronize()
+        out: dict = {}
+        for name, s, e in self.records:
+            out.setdefault(name, []).append(s.elapsed_time(e))
+        return out
+
+
+_timer: Optional[KernelTimer] = None
+
+
+@contextlib.contextmanager
+def kernel_timing(timer: KernelTimer):
+    """Within the block, every launcher call records its kernels on ``timer``."""
+    global _timer
+    prev, _timer = _timer, timer
+    try:
+        yield timer
+    finally:
+        _timer = prev
+
+
+def _events(names):
+    if _timer is None:
+        return None
+    return _timer.take(names)
+
+
+def _workspace(fn, prob: _capi.Problem, dev) -> torch.Tensor:
+    nbytes = int(fn(ctypes.byref(prob)))
+    return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+
+
+def _run_fwd(prob, q, k, v, r_q, r_k, gs, out, lse, view):
+    L = _capi.lib()
+    ws = _workspace(L.fna2_fwd_workspace_bytes, prob, q.device)
+    ev = _events(KernelTimer.FWD)
+    args = _capi.FwdArgs(prob, view(q), view(k), view(v), view(r_q), view(r_k), _ptr(gs),
+                         view(out), view(lse), ws.data_ptr(), ws.numel(),
+                         ctypes.cast(ev, ctypes.c_void_p) if ev is not None else None)
+    with torch.cuda.device(q.device):
+        st = L.fna2_fwd(ctypes.byref(args), _stream(q.device))
+    _capi.raise_for(st, "fna2_fwd")
+
+
+def _run_bwd(prob, tensors, view):
+    (dout, q, k, v, r_q, r_k, gs, out, lse, delta, dq, dk, dv, dr_q, dr_k, d_gs) = tensors
+    L = _capi.lib()
+    ws = _workspace(L.fna2_bwd_workspace_bytes, prob, q.device)
+    ev = _events(KernelTimer.BWD)
+    args = _capi.BwdArgs(prob, view(q), view(k), view(v), view(r_q), view(r_k), _ptr(gs),
+                         view(out), view(lse), view(dout), view(delta), view(dq), view(dk),
+                         view(dv), view(dr_q), view(dr_k), _ptr(d_gs), ws.data_ptr(), ws.numel(),
+                         ctypes.cast(ev, ctypes.c_void_p) if ev is not None else None)
+    with torch.cuda.device(q.device):
+        st = L.fna2_bwd(ctypes.byref(args), _stream(q.device))
+    _capi.raise_for(st, "fna2_bwd")
+
+
+# ─────────────────────────────────────────────────────────────────────────────
+# launchers (same names and signatures as the reference)
+# ─────────────────────────────────────────────────────────────────────────────
+
+def _fna2_forward(
+    q: torch.Tensor,            # [B, H, S, D]
+    k: torch.Tensor,            # [B, H_KV, S_k, D]
+    v: torch.Tensor,            # [B, H_KV, S_k, D]
+    r_q: Optional[torch.Tensor],  # [B, H_G, S, R]
+    r_k: Optional[torch.Tensor],  # [B, H_G, S_k, R]
+    graph_scale: Optional[torch.Tensor],  # [H_G]
+    softmax_scale: float,
+    is_causal: bool,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Dense forward; returns (out, lse).  Mirrors FNA2/flash_naylis_attn.py:700-753."""
+    B, H, S, D = q.shape
+    H_KV, S_k = k.shape[1], k.shape[2]
+    H_G = 0 if r_q is None else r_q.shape[1]
+    R = 0 if r_q is None else r_q.shape[3]
+    if r_q is not None:
+        assert H_G == r_k.shape[1], "r_q and r_k must have the same number of graph heads"
+        assert H_G == 0 or rank_supported(R), \
+            f"rel_rank must be a multiple of 8 in [8, 64] (got {R})"
+    assert D in SUPPORTED_HEAD_DIMS, f"head_dim must be 64 or 128 (got {D})"
+    assert H % H_KV == 0, f"num heads {H} must be a multiple of KV heads {H_KV}"
+    _check_inputs(q, k, v, r_q, r_k, graph_scale)
+    q, k, v, r_q, r_k = (_prep(t) for t in (q, k, v, r_q, r_k))
+    gs = _gs32(graph_scale) if H_G else None
+    out = torch.empty_like(q)
+    lse = torch.empty(B, H, S, device=q.device, dtype=torch.float32)
+    prob = _problem(False, B, S, S_k, 0, 0, H, H_KV, H_G, D, R, is_causal, softmax_scale)
+    _run_fwd(prob, q, k, v, r_q if H_G else None, r_k if H_G else None, gs, out, lse, _view4)
+    return out, lse
+
+
+def _fna2_forward_varlen(
+    q: torch.Tensor,            # [T, H, D]
+    k: torch.Tensor,            # [T_k, H_KV, D]
+    v: torch.Tensor,            # [T_k, H_KV, D]
+    r_q: Optional[torch.Tensor],  # [T, H_G, R]
+    r_k: Optional[torch.Tensor],  # [T_k, H_G, R]
+    graph_scale: Optional[torch.Tensor],  # [H_G]
+    cu_seqlens_q: torch.Tensor,  # [N + 1] int32
+    cu_seqlens_k: torch.Tensor,  # [N + 1] int32
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    softmax_scale: float,
+    is_causal: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Varlen forward; returns (out [T,H,D], lse [T,H]).  Mirrors :756-804."""
+    total_q, H, D = q.shape
+    total_k, H_KV = k.shape[0], k.shape[1]
+    H_G = 0 if r_q is None else r_q.shape[1]
+    R = 0 if r_q is None else r_q.shape[2]
+    N = cu_seqlens_q.shape[0] - 1
+    if r_q is not None:
+        assert H_G == r_k.shape[1], "r_q and r_k must have the same number of graph heads"
+        assert H_G == 0 or rank_supported(R), \
+            f"rel_rank must be a multiple of 8 in [8, 64] (got {R})"
+    assert D in SUPPORTED_HEAD_DIMS, f"head_dim must be 64 or 128 (got {D})"
+    assert H % H_KV == 0, f"num heads {H} must be a multiple of KV heads {H_KV}"
+    assert cu_seqlens_k.shape[0] == N + 1, "cu_seqlens_q and cu_seqlens_k differ in length"
+    _check_inputs(q, k, v, r_q, r_k, graph_scale)
+    q, k, v, r_q, r_k = (_prep(t) for t in (q, k, v, r_q, r_k))
+    cu_q = cu_seqlens_q.to(device=q.device, dtype=torch.int32).contiguous()
+    cu_k = cu_seqlens_k.to(device=q.device, dtype=torch.int32).contiguous()
+    gs = _gs32(graph_scale) if H_G else None
+    out = torch.empty_like(q)
+    lse = torch.empty(total_q, H, device=q.device, dtype=torch.float32)
+    prob = _problem(True, N, max_seqlen_q, max_seqlen_k, total_q, total_k, H, H_KV, H_G, D, R,
+                    is_causal, softmax_scale, cu_q, cu_k)
+    _run_fwd(prob, q, k, v, r_q if H_G else None, r_k if H_G else None, gs, out, lse, _view3)
+    return out, lse
+
+
+def _grads_like(q, k, v, r_q, r_k, H_G):
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    dr_q = torch.empty_like(r_q) if H_G else None
+    dr_k = torch.empty_like(r_k) if H_G else None
+    return dq, dk, dv, dr_q, dr_k
+
+
+def _fna2_backward(
+    dout: torch.Tensor,
+    q, k, v, r_q, r_k, graph_scale,
+    out, lse,
+    softmax_scale: float,
+    is_causal: bool,
+) -> tuple:
+    """Dense backward; returns (dq, dk, dv, dr_q, dr_k, d_gs).  Mirrors :807-892."""
+    B, H, S, D = q.shape
+    H_KV, S_k = k.shape[1], k.shape[2]
+    H_G = 0 if r_q is None else r_q.shape[1]
+    R = 0 if r_q is None else r_q.shape[3]
+    dout = _prep(dout)
+    q, k, v, r_q, r_k, out = (_prep(t) for t in (q, k, v, r_q, r_k, out))
+    gs = _gs32(graph_scale) if H_G else None
+    lse = lse.contiguous()
+    delta = torch.empty(B, H, S, device=q.device, dtype=torch.float32)
+    dq, dk, dv, dr_q, dr_k = _grads_like(q, k, v, r_q, r_k, H_G)
+    d_gs = torch.empty(max(H_G, 1), device=q.device, dtype=torch.float32)
+    prob = _problem(False, B, S, S_k, 0, 0, H, H_KV, H_G, D, R, is_causal, softmax_scale)
+    _run_bwd(prob, (dout, q, k, v, r_q if H_G else None, r_k if H_G else None, gs, out, lse,
+                    delta, dq, dk, dv, dr_q, dr_k, d_gs if H_G else None), _view4)
+    return dq, dk, dv, dr_q, dr_k, _dgs_out(d_gs, H_G, graph_scale)
+
+
+def _fna2_backward_varlen(
+    dout: torch.Tensor,
+    q, k, v, r_q, r_k, graph_scale,
+    out, lse,
+    cu_seqlens_q: torch.Tensor,
+    cu_seqlens_k: torch.Tensor,
+    max_seqlen_q: int,
+    max_seqlen_k: int,
+    softmax_scale: float,
+    is_causal: bool = True,
+) -> tuple:
+    """Varlen backward; returns (dq, dk, dv, dr_q, dr_k, d_gs).  Mirrors :1215-1300."""
+    total_q, H, D = q.shape
+    total_k, H_KV = k.shape[0], k.shape[1]
+    H_G = 0 if r_q is None else r_q.shape[1]
+    R = 0 if r_q is None else r_q.shape[2]
+    N = cu_seqlens_q.shape[0] - 1
+    dout = _prep(dout)
+    q, k, v, r_q, r_k, out = (_prep(t) for t in (q, k, v, r_q, r_k, out))
+    cu_q = cu_seqlens_q.to(device=q.device, dtype=torch.int32).contiguous()
+    cu_k = cu_seqlens_k.to(device=q.device, dtype=torch.int32).contiguous()
+    gs = _gs32(graph_scale) if H_G else None
+    lse = lse.contiguous()
+    delta = torch.empty(total_q, H, device=q.device, dtype=torch.float32)
+    dq, dk, dv, dr_q, dr_k = _grads_like(q, k, v, r_q, r_k, H_G)
+    d_gs = torch.empty(max(H_G, 1), device=q.device, dtype=torch.float32)
+    prob = _problem(True, N, max_seqlen_q, max_seqlen_k, total_q, total_k, H, H_KV, H_G, D, R,
+                    is_causal, softmax_scale, cu_q, cu_k)
+    _run_bwd(prob, (dout, q, k, v, r_q if H_G else None, r_k if H_G else None, gs, out, lse,
+                    delta, dq, dk, dv, dr_q, dr_k, d_gs if H_G else None), _view3)
+    return dq, dk, dv, dr_q, dr_k, _dgs_out(d_gs, H_G, graph_scale)
+
+
+def _dgs_out(d_gs, H_G, graph_scale):
+    if not H_G or graph_scale is None:
+        return None
+    return d_gs[:H_G].to(graph_scale.dtype)
+
+
+# ─────────────────────────────────────────────────────────────────────────────
+# autograd
+# ─────────────────────────────────────────────────────────────────────────────
+
+class FlashNaylisAttnFunc(torch.autograd.Function):
+    """autograd wrapper, same contract as FNA2/flash_naylis_attn.py:1307-1373."""
+
+    @staticmethod
+    def forward(
+        ctx,
+        q, k, v, r_q, r_k, graph_scale,
+        softmax_scale: float,
+        is_causal: bool,
+        cu_seqlens_q=None,
+        cu_seqlens_k=None,
+        max_seqlen_q: int = 0,
+        max_seqlen_k: int = 0,
+    ):
+        use_varlen = cu_seqlens_q is not None
+        if use_varlen:
+            if cu_seqlens_k is None:
+                cu_seqlens_k = cu_seqlens_q
+            out, lse = _fna2_forward_varlen(
+                q, k, v, r_q, r_k, graph_scale,
+                cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                softmax_scale, is_causal,
+            )
+        else:
+            out, lse = _fna2_forward(q, k, v, r_q, r_k, graph_scale, softmax_scale, is_causal)
+        ctx.save_for_backward(q, k, v, r_q, r_k, graph_scale, out, lse)
+        ctx.softmax_scale = softmax_scale
+        ctx.is_causal = is_causal
+        ctx.use_varlen = use_varlen
+        ctx.cu_seqlens_q = cu_seqlens_q
+        ctx.cu_seqlens_k = cu_seqlens_k
+        ctx.max_seqlen_q = max_seqlen_q
+        ctx.max_seqlen_k = max_seqlen_k
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, r_q, r_k, graph_scale, out, lse = ctx.saved_tensors
+        if ctx.use_varlen:
+            grads = _fna2_backward_varlen(
+                dout, q, k, v, r_q, r_k, graph_scale, out, lse,
+                ctx.cu_seqlens_q, ctx.cu_seqlens_k, ctx.max_seqlen_q, ctx.max_seqlen_k,
+                ctx.softmax_scale, ctx.is_causal,
+            )
+        else:
+            grads = _fna2_backward(
+                dout, q, k, v, r_q, r_k, graph_scale, out, lse,
+                ctx.softmax_scale, ctx.is_causal,
+            )
+        dq, dk, dv, dr_q, dr_k, d_gs = grads
+        return dq, dk, dv, dr_q, dr_k, d_gs, None, None, None, None, None, None
+
+
+# ─────────────────────────────────────────────────────────────────────────────
+# public API
+# ─────────────────────────────────────────────────────────────────────────────
+
+def flash_naylis_attn(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    r_q: Optional[torch.Tensor],
+    r_k: Optional[torch.Tensor],
+    graph_scale: Optional[torch.Tensor],
+    softmax_scale: Optional[float] = None,
+    is_causal: bool = True,
+    cu_seqlens_q: Optional[torch.Tensor] = None,
+    cu_seqlens_k: Optional[torch.Tensor] = None,
+    max_seqlen_q: int = 0,
+    max_seqlen_k: int = 0,
+) -> torch.Tensor:
+    """FlashNaylisAttention-2 (FNA2/flash_naylis_attn.py:1380-1434).
+
+    q, k, v       dense [B, H, S, D] / [B, H_KV, S_k, D] (any strides with a
+                  unit last stride) or varlen [T, H, D] / [T_k, H_KV, D]
+    r_q, r_k      dense [B, H_G, S, R] or varlen [T, H_G, R], bfloat16; heads
+                  [0, H_G) get the bias graph_scale[h] * R_q R_k^T
+    graph_scale   [H_G]
+    softmax_scale 1/sqrt(D) if None
+    is_causal     top-left causal mask on local positions
+    cu_seqlens_*  varlen offsets (int32); max_seqlen_* are scheduling hints
+
+    Returns the attention output with q's shape, dtype and strides.
+    """
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+    if r_q is not None:
+        assert r_q.dtype == torch.bfloat16, "r_q must be bfloat16"
+        assert r_k is not None and r_k.dtype == torch.bfloat16, "r_k must be bfloat16"
+        R = r_q.shape[-1]
+        assert rank_supported(R), f"rel_rank must be a multiple of 8 in [8, 64] (got {R})"
+    return FlashNaylisAttnFunc.apply(
+        q, k, v, r_q, r_k, graph_scale,
+        softmax_scale, is_causal,
+        cu_seqlens_q, cu_seqlens_k,
+        max_seqlen_q, max_seqlen_k,
+    )

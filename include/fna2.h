@@ -1,0 +1,162 @@
+/*
+ * fna2.h — C ABI of the MI355X (gfx950) FlashNaylisAttention-2 kernels.
+ *
+ * Attention score, per sequence and query head h (KV head h / (H / H_KV)):
+ *
+ *     S[i][j] = softmax_scale * <Q_i, K_j> + [h < H_G] * graph_scale[h] * <Rq_i, Rk_j>
+ *
+ * masked to -inf where j > i (causal, top-left aligned local positions) or
+ * j >= len_k.  O_i = sum_j exp(S_ij - m_i) V_j / (l_i + 1e-6) and
+ * LSE_i = m_i + log(l_i + 1e-6), as in the reference kernels
+ * (myAiByMe/FNA2 FNA2/flash_naylis_attn.py:192-195, :340-345).
+ *
+ * Every entry point takes plain device pointers, element strides and sizes.
+ * The library never allocates device memory: the caller owns every output
+ * and the workspace (size it with fna2_*_workspace_bytes).  Kernels are
+ * launched on the stream given; no call synchronises the host.  All entry
+ * points are stateless and reentrant.  A nonzero return means nothing was
+ * launched (FNA2_E_LAUNCH: a launch failed after earlier launches of the
+ * same call may already have run).
+ *
+ * Layout.  Each tensor X is described by a base pointer and three element
+ * strides (stride_b, stride_s, stride_h); the innermost (feature) stride
+ * must be 1.  Dense mode (varlen == 0): element [b, h, s, f] lives at
+ * X + b*stride_b + s*stride_s + h*stride_h + f.  Varlen mode: element
+ * [t, h, f] of packed token t lives at X + t*stride_s + h*stride_h + f and
+ * sequence b covers tokens [cu_seqlens[b], cu_seqlens[b+1]); stride_b is
+ * ignored.  LSE and delta (fp32) use the same scheme with a feature size of 1.
+ */
+#ifndef FNA2_H_
+#define FNA2_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FNA2_ABI_VERSION 1
+
+/* Element type of q, k, v, r_q, r_k, out, dout and of the gradients. */
+enum fna2_dtype { FNA2_BF16 = 1 };
+
+/* Return codes. */
+enum fna2_status {
+  FNA2_OK = 0,
+  FNA2_E_NULL = -1,        /* a required pointer is NULL                     */
+  FNA2_E_DTYPE = -2,       /* unsupported element type                       */
+  FNA2_E_HEAD_DIM = -3,    /* head_dim not in {64, 128}                      */
+  FNA2_E_RANK = -4,        /* rank not a multiple of 8 in [8, 64]            */
+  FNA2_E_HEADS = -5,       /* heads / heads_kv / heads_graph inconsistent    */
+  FNA2_E_SHAPE = -6,       /* negative or zero-sized extent, or overflow     */
+  FNA2_E_STRIDE = -7,      /* stride or pointer not 16-byte aligned          */
+  FNA2_E_SEQLENS = -8,     /* varlen without cu_seqlens                      */
+  FNA2_E_WORKSPACE = -9,   /* workspace missing or too small                 */
+  FNA2_E_LAUNCH = -10,     /* a kernel launch failed                         */
+  FNA2_E_DEVICE = -11,     /* current device is not gfx950                   */
+  FNA2_E_SCALE = -12       /* softmax_scale not finite                       */
+};
+
+/* A bf16/fp32 tensor view: base pointer + element strides. */
+typedef struct fna2_tensor {
+  void* ptr;
+  int64_t stride_b; /* dense only */
+  int64_t stride_s;
+  int64_t stride_h;
+} fna2_tensor;
+
+/* Problem shape shared by the forward and the backward. */
+typedef struct fna2_problem {
+  int32_t dtype;       /* enum fna2_dtype */
+  int32_t varlen;      /* 0 dense [B,H,S,*], 1 packed [T,H,*] with cu_seqlens */
+  int32_t batch;       /* dense: B; varlen: number of sequences N            */
+  int32_t seqlen_q;    /* dense: S_q; varlen: max_seqlen_q (a scheduling hint) */
+  int32_t seqlen_k;    /* dense: S_k; varlen: max_seqlen_k (a scheduling hint) */
+  int32_t total_q;     /* varlen: token count of q/out (bounds every access) */
+  int32_t total_k;     /* varlen: token count of k/v                         */
+  int32_t heads;       /* H: query heads                                     */
+  int32_t heads_kv;    /* H_KV: divides H (GQA)                              */
+  int32_t heads_graph; /* H_G <= H: heads [0, H_G) carry the low-rank bias   */
+  int32_t head_dim;    /* D in {64, 128}                                     */
+  int32_t rank;        /* R: multiple of 8 in [8, 64] (ignored if H_G == 0)  */
+  int32_t causal;      /* 1: key j visible to query i iff j <= i             */
+  float softmax_scale;
+  const int32_t* cu_seqlens_q; /* varlen: [N+1] device int32               */
+  const int32_t* cu_seqlens_k; /* varlen: [N+1] device int32               */
+} fna2_problem;
+
+typedef struct fna2_fwd_args {
+  fna2_problem p;
+  fna2_tensor q;   /* [.., H,    D] */
+  fna2_tensor k;   /* [.., H_KV, D] */
+  fna2_tensor v;   /* [.., H_KV, D] */
+  fna2_tensor r_q; /* [.., H_G,  R] */
+  fna2_tensor r_k; /* [.., H_G,  R] */
+  const float* graph_scale; /* [H_G] fp32 */
+  fna2_tensor out; /* [.., H, D], written */
+  fna2_tensor lse; /* fp32 [.., H] (feature size 1), written */
+  void* workspace;
+  size_t workspace_bytes;
+  /* Optional (may be NULL): FNA2_FWD_EVENTS hipEvent_t handles owned by the
+   * caller; recorded on the stream immediately before and after the
+   * attention kernel, for per-kernel timing. */
+  void* const* events;
+} fna2_fwd_args;
+
+#define FNA2_FWD_EVENTS 2 /* attention kernel start, end */
+#define FNA2_BWD_EVENTS 6 /* delta start/end, dK-dV start/end, dQ start/end */
+
+typedef struct fna2_bwd_args {
+  fna2_problem p;
+  fna2_tensor q, k, v, r_q, r_k;
+  const float* graph_scale;
+  fna2_tensor out;   /* forward output                 */
+  fna2_tensor lse;   /* forward LSE (fp32)             */
+  fna2_tensor dout;  /* upstream gradient, like out    */
+  fna2_tensor delta; /* fp32 scratch like lse, written */
+  fna2_tensor dq;    /* like q,   written              */
+  fna2_tensor dk;    /* like k,   written              */
+  fna2_tensor dv;    /* like v,   written              */
+  fna2_tensor dr_q;  /* like r_q, written              */
+  fna2_tensor dr_k;  /* like r_k, written              */
+  float* d_graph_scale; /* [H_G] fp32, written         */
+  void* workspace;
+  size_t workspace_bytes;
+  /* Optional (may be NULL): FNA2_BWD_EVENTS hipEvent_t handles owned by the
+   * caller, recorded around the delta, dK/dV/dRk and dQ/dRq kernels. */
+  void* const* events;
+} fna2_bwd_args;
+
+/* ABI version (FNA2_ABI_VERSION). */
+int fna2_version(void);
+
+/* Static text for a status code. */
+const char* fna2_status_string(int status);
+
+/* Host-only validation of shapes, strides, alignment and pointers; no GPU
+ * call.  Replaces the reference launchers' asserts
+ * (FNA2/flash_naylis_attn.py:718-720, :778). */
+int fna2_check_fwd(const fna2_fwd_args* args);
+int fna2_check_bwd(const fna2_bwd_args* args);
+
+/* Workspace bytes the forward / backward need for this problem. */
+size_t fna2_fwd_workspace_bytes(const fna2_problem* p);
+size_t fna2_bwd_workspace_bytes(const fna2_problem* p);
+
+/* Forward: writes out and lse.
+ * Replaces _fna2_forward (FNA2/flash_naylis_attn.py:700-753) and
+ * _fna2_forward_varlen (FNA2/flash_naylis_attn.py:756-804). */
+int fna2_fwd(const fna2_fwd_args* args, void* hip_stream);
+
+/* Backward: writes delta, dq, dk, dv, dr_q, dr_k and d_graph_scale
+ * (no pre-zeroing needed; no atomics; bitwise deterministic).
+ * Replaces _fna2_backward (FNA2/flash_naylis_attn.py:807-892) and
+ * _fna2_backward_varlen (FNA2/flash_naylis_attn.py:1215-1300). */
+int fna2_bwd(const fna2_bwd_args* args, void* hip_stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FNA2_H_ */

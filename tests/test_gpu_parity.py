@@ -1,0 +1,191 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the fp64 CPU oracle.
+
+Small and medium shapes covering the reference's configurations (dense and
+varlen, causal and not, GQA, vanilla heads, every supported rank and head
+dim), run on the same seeded bf16 inputs.  Tolerances: out 2e-2 max abs,
+gradients 5e-2 relative norm, LSE 1e-2 max abs.
+"""
+import importlib
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from tests import helpers as H
+
+pytestmark = pytest.mark.gpu
+
+
+def _fna2():
+    return importlib.import_module("fna2_amd.flash_naylis_attn")
+
+
+def _dense_case(gpu, B, Hq, S, D, H_KV, H_G, R, causal, seed, Sk=None, layout="bhsd", gs=None):
+    F = _fna2()
+    q, k, v, rq, rk, gs_, dout = H.make_dense(B, Hq, S, D, H_KV, H_G, R, seed=seed, Sk=Sk,
+                                              layout=layout, gs=gs)
+    scale = 1.0 / math.sqrt(D)
+    print(f"dense B{B} H{Hq} S{S} Sk{Sk} D{D} HKV{H_KV} HG{H_G} R{R} causal={causal}", flush=True)
+    dq_ = [t.to(gpu) if t is not None else None for t in (q, k, v, rq, rk, gs_, dout)]
+    out, lse = F._fna2_forward(dq_[0], dq_[1], dq_[2], dq_[3], dq_[4], dq_[5], scale, causal)
+    grads = F._fna2_backward(dq_[6], dq_[0], dq_[1], dq_[2], dq_[3], dq_[4], dq_[5], out, lse,
+                             scale, causal)
+    torch.cuda.synchronize()
+    ref_out, ref_lse, ref_g = H.oracle_fwd_bwd(q, k, v, rq, rk, gs_, dout, scale, causal)
+    H.check_out(out, lse, ref_out, ref_lse)
+    return H.check_grads(grads, ref_g)
+
+
+@pytest.mark.parametrize("D,R", [(64, 16), (128, 32), (64, 8), (128, 64), (64, 64), (128, 16),
+                                 (128, 24), (64, 48)])
+def test_dense_causal_ranks(gpu, D, R):
+    _dense_case(gpu, 2, 4, 200, D, 4, 4, R, True, seed=D + R)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_dense_gqa_vanilla(gpu, causal):
+    # reference validation config "60m": B2 H8 S128 D64 H_KV4 H_G4 R32
+    _dense_case(gpu, 2, 8, 128, 64, 4, 4, 32, causal, seed=42)
+
+
+def test_dense_220m_config(gpu):
+    # reference validation config "220m": B2 H12 S256 D64 H_KV4 H_G8 R32
+    _dense_case(gpu, 2, 12, 256, 64, 4, 8, 32, True, seed=42)
+
+
+def test_dense_no_graph_heads(gpu):
+    _dense_case(gpu, 1, 4, 300, 128, 2, 0, 0, True, seed=3)
+
+
+@pytest.mark.parametrize("S,Sk", [(1, 1), (65, 65), (129, 97), (96, 200), (333, 333)])
+def test_dense_odd_lengths(gpu, S, Sk):
+    _dense_case(gpu, 1, 2, S, 64, 2, 2, 16, True, seed=S, Sk=Sk)
+    _dense_case(gpu, 1, 2, S, 128, 1, 1, 32, False, seed=S + 1, Sk=Sk)
+
+
+def test_dense_strided_layout(gpu):
+    # [B, S, H, D] memory passed as [B, H, S, D] views, as the configs state
+    _dense_case(gpu, 2, 4, 256, 128, 4, 4, 32, True, seed=5, layout="bshd")
+
+
+def test_scale_edge_cases(gpu):
+    F = _fna2()
+    q, k, v, rq, rk, gs, dout = H.make_dense(1, 2, 96, 64, 2, 2, 16, seed=9)
+    for scale in (0.0, -0.125, 0.5):
+        qg, kg, vg, rqg, rkg, gsg, dog = (t.to(gpu) for t in (q, k, v, rq, rk, gs, dout))
+        out, lse = F._fna2_forward(qg, kg, vg, rqg, rkg, gsg, scale, True)
+        grads = F._fna2_backward(dog, qg, kg, vg, rqg, rkg, gsg, out, lse, scale, True)
+        torch.cuda.synchronize()
+        ro, rl, rg = H.oracle_fwd_bwd(q, k, v, rq, rk, gs, dout, scale, True)
+        H.check_out(out, lse, ro, rl)
+        H.check_grads(grads, rg)
+
+
+def _varlen_case(gpu, lengths, Hq, D, H_KV, H_G, R, causal, seed, lengths_k=None, gs=None,
+                 r_std=None):
+    F = _fna2()
+    (q, k, v, rq, rk, gs_, dout, cu_q, cu_k) = H.make_varlen(
+        lengths, Hq, D, H_KV, H_G, R, seed=seed, lengths_k=lengths_k, gs=gs, r_std=r_std)
+    scale = 1.0 / math.sqrt(D)
+    print(f"varlen n={len(lengths)} T={sum(lengths)} H{Hq} D{D} HKV{H_KV} HG{H_G} R{R} "
+          f"causal={causal}", flush=True)
+    g = [t.to(gpu) if t is not None else None for t in (q, k, v, rq, rk, gs_, dout, cu_q, cu_k)]
+    mq = max(lengths) if lengths else 0
+    mk = max(lengths_k or lengths) if (lengths_k or lengths) else 0
+    out, lse = F._fna2_forward_varlen(g[0], g[1], g[2], g[3], g[4], g[5], g[7], g[8], mq, mk,
+                                      scale, causal)
+    grads = F._fna2_backward_varlen(g[6], g[0], g[1], g[2], g[3], g[4], g[5], out, lse, g[7],
+                                    g[8], mq, mk, scale, causal)
+    torch.cuda.synchronize()
+    ref_out, ref_lse, ref_g = H.oracle_fwd_bwd(q, k, v, rq, rk, gs_, dout, scale, causal,
+                                               cu_q.numpy(), cu_k.numpy())
+    H.check_out(out, lse, ref_out, ref_lse)
+    return H.check_grads(grads, ref_g)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_varlen_mixed(gpu, causal):
+    lengths = [1, 17, 64, 127, 128, 129, 300, 5, 257]
+    _varlen_case(gpu, lengths, 4, 128, 2, 3, 32, causal, seed=11)
+    _varlen_case(gpu, lengths, 4, 64, 4, 4, 16, causal, seed=12)
+
+
+def test_varlen_cross_lengths(gpu):
+    lq = [50, 130, 7, 200]
+    lk = [70, 100, 7, 260]
+    _varlen_case(gpu, lq, 2, 64, 2, 2, 16, True, seed=13, lengths_k=lk)
+    _varlen_case(gpu, lq, 2, 128, 1, 2, 32, False, seed=14, lengths_k=lk)
+
+
+def test_varlen_empty_sequences(gpu):
+    _varlen_case(gpu, [0, 40, 0, 0, 90, 0], 2, 64, 2, 2, 16, True, seed=15)
+
+
+def test_varlen_bias_dominated(gpu):
+    # c5-like: rank 16 bias with R std 0.5 and non-causal attention
+    _varlen_case(gpu, [300, 16, 128, 40, 77], 4, 64, 4, 4, 16, False, seed=16, gs=1.0,
+                 r_std=0.5)
+
+
+def test_varlen_matches_per_segment_dense(gpu):
+    """Reference T3/T3b: packed == per-segment dense (flash_naylis_attn path only)."""
+    F = _fna2()
+    lengths = [64, 64]
+    (q, k, v, rq, rk, gs, dout, cu_q, cu_k) = H.make_varlen(lengths, 8, 64, 4, 4, 32, seed=99,
+                                                            device=gpu)
+    scale = 0.125
+    qs = [t.clone().requires_grad_(True) for t in (q, k, v, rq, rk, gs)]
+    out_p = F.flash_naylis_attn(*qs, softmax_scale=scale, is_causal=True, cu_seqlens_q=cu_q,
+                                cu_seqlens_k=cu_k, max_seqlen_q=64, max_seqlen_k=64)
+    out_p.float().sum().backward()
+    outs, grads = [], [[] for _ in range(5)]
+    dgs = torch.zeros_like(gs)
+    for s0, s1 in ((0, 64), (64, 128)):
+        seg = [t[s0:s1].detach().clone().requires_grad_(True) for t in (q, k, v, rq, rk)]
+        g_s = gs.detach().clone().requires_grad_(True)
+        r4 = [t.transpose(0, 1).unsqueeze(0) for t in seg]
+        o = F.flash_naylis_attn(*r4, g_s, softmax_scale=scale, is_causal=True)
+        o.float().sum().backward()
+        outs.append(o.squeeze(0).transpose(0, 1))
+        for i in range(5):
+            grads[i].append(seg[i].grad)
+        dgs += g_s.grad
+    ref = torch.cat(outs, 0)
+    assert H.max_abs(out_p, ref) < 1e-2
+    for i in range(5):
+        assert H.rel_norm(qs[i].grad, torch.cat(grads[i], 0)) < 1e-2
+    assert H.rel_norm(qs[5].grad, dgs) < 1e-2
+
+
+def test_gs_zero_equals_sdpa(gpu):
+    """Reference T4: graph_scale = 0 gives plain causal attention (torch SDPA)."""
+    F = _fna2()
+    q, k, v, rq, rk, gs, _ = H.make_dense(2, 8, 128, 64, 4, 4, 32, seed=7, gs=0.0, device=gpu)
+    out = F.flash_naylis_attn(q, k, v, rq, rk, gs, softmax_scale=0.125, is_causal=True)
+    ke = k.float().repeat_interleave(2, dim=1)
+    ve = v.float().repeat_interleave(2, dim=1)
+    ref = torch.nn.functional.scaled_dot_product_attention(q.float(), ke, ve, is_causal=True,
+                                                           scale=0.125)
+    assert H.max_abs(out, ref) < 2e-2
+
+
+def test_deterministic(gpu):
+    F = _fna2()
+    q, k, v, rq, rk, gs, dout = H.make_dense(2, 4, 384, 128, 2, 4, 32, seed=21, device=gpu)
+    res = []
+    for _ in range(2):
+        out, lse = F._fna2_forward(q, k, v, rq, rk, gs, 0.088, True)
+        g = F._fna2_backward(dout, q, k, v, rq, rk, gs, out, lse, 0.088, True)
+        res.append([out, lse, *g])
+    torch.cuda.synchronize()
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+
+
+def test_row0_equals_v0(gpu):
+    """Causal row 0 attends only to key 0: O_0 = V_0 (to bf16 rounding)."""
+    F = _fna2()
+    q, k, v, rq, rk, gs, _ = H.make_dense(1, 2, 64, 64, 2, 2, 16, seed=4, device=gpu)
+    out, _ = F._fna2_forward(q, k, v, rq, rk, gs, 0.125, True)
+    assert H.max_abs(out[:, :, 0], v[:, :, 0]) < 1e-2
