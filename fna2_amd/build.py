@@ -71,6 +71,11 @@ def build(verbose: bool = False, jobs: int = 4) -> Path:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
+    # The library must load (an unresolved host symbol would only show at dlopen).
+    chk = subprocess.run([sys.executable, "-c", f"import ctypes; ctypes.CDLL({str(tmp)!r})"],
+                         capture_output=True, text=True)
+    if chk.returncode != 0:
+        raise RuntimeError(f"built library does not load:\n{chk.stderr.strip()}")
     os.replace(tmp, LIB)
     return LIB
 

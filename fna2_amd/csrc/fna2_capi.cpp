@@ -325,9 +325,9 @@ int fna2_fwd(const fna2_fwd_args* a, void* stream_ptr) {
     K.tiles = tiles;
     K.n_tiles = count;
   }
-  const int rp = fna2::padded_rank(K.p.H_G, K.p.R);
+  const int rpl = fna2::padded_rank32(K.p.H_G, K.p.R);
   if (!mark(a->events, 0, stream)) return FNA2_E_LAUNCH;
-  if (fna2::launch_fwd(K, rp, (int)g.fwd_grid, stream) != hipSuccess) return FNA2_E_LAUNCH;
+  if (fna2::launch_fwd(K, rpl, (int)g.fwd_grid, stream) != hipSuccess) return FNA2_E_LAUNCH;
   if (!mark(a->events, 1, stream)) return FNA2_E_LAUNCH;
   return FNA2_OK;
 }

@@ -61,6 +61,10 @@ struct SeqExt {
   int q0, lq, k0, lk;
 };
 
+// Marks a value that is the same in every lane as wave-uniform (scalar).
+__device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// Extents of sequence b (b may differ per lane).
 __device__ __forceinline__ SeqExt seq_ext(const Problem& p, int b) {
   SeqExt e;
   if (p.varlen) {
@@ -75,6 +79,17 @@ __device__ __forceinline__ SeqExt seq_ext(const Problem& p, int b) {
     e.q0 = 0; e.lq = p.sq; e.k0 = 0; e.lk = p.sk;
   }
   return e;
+}
+
+// Extents of a sequence b that is the same in every lane (scalar registers).
+__device__ __forceinline__ SeqExt seq_ext_uniform(const Problem& p, int b) {
+  const SeqExt e = seq_ext(p, b);
+  SeqExt u;
+  u.q0 = uni(e.q0);
+  u.lq = uni(e.lq);
+  u.k0 = uni(e.k0);
+  u.lk = uni(e.lk);
+  return u;
 }
 
 // Base pointer of sequence b, head h of a view; row r is at base + r * ss.

@@ -41,6 +41,12 @@ inline int padded_rank(int H_G, int R) {
   return (H_G > 0 && R > 0) ? ((R + 15) / 16) * 16 : 0;
 }
 
+// Rank padded to a multiple of 32 (the LDS tile width of the rank part of a
+// key or query tile): 0, 32 or 64.
+inline int padded_rank32(int H_G, int R) {
+  return (H_G > 0 && R > 0) ? ((R + 31) / 32) * 32 : 0;
+}
+
 hipError_t launch_fwd(const FwdParams& P, int rp, int grid, hipStream_t s);
 hipError_t launch_bwd_delta(const BwdParams& P, hipStream_t s);
 hipError_t launch_bwd_dkdv(const BwdParams& P, int rp, int grid, hipStream_t s);
