@@ -36,7 +36,8 @@ COMMON = [
     f"-I{CSRC}",
 ]
 
-SOURCES = ["fna2_capi.cpp", "fna2_sched.hip", "fna2_fwd.hip", "fna2_bwd.hip"]
+SOURCES = ["fna2_capi.cpp", "fna2_sched.hip", "fna2_fwd.hip", "fna2_bwd.hip", "fna2_bwd_dkdv.hip",
+           "fna2_bwd_dq.hip"]
 
 
 def _compile(src: Path, obj: Path, verbose: bool) -> None:

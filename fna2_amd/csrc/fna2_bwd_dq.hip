@@ -1,0 +1,289 @@
+// fna2_bwd_dq.hip — dQ, dRq and the d_graph_scale partials for gfx950.
+//
+// Replaces _fna2_bwd_dq_kernel / _fna2_bwd_dq_varlen_kernel
+// (FNA2/flash_naylis_attn.py:561-693, :1085-1208); d_graph_scale, which the
+// reference accumulates in its dK/dV kernel (:537-538, :553), is formed here.
+//
+// One workgroup = 4 waves = 128 queries of one (sequence, head); wave w owns
+// queries 32w..32w+31 with Qa = [a Q | bf16(b Rq)] and dO rows in registers.
+// Per 64-key step (keys stream in by DMA through a two-stage ring):
+//   S^T, dP^T  (64 keys x 32 queries)   A operands: K | Rk and V rows (LDS)
+//   dA^T = c P^T (dP^T - delta)
+//   dQa^T += Ka^T dA^T = [dQ / a | dRq / b]^T   A operand: (K | Rk)^T by
+//                                             transpose reads
+// d_gs = (1/c) sum_i <Rq_i, (dA Rk)_i> is reduced per workgroup into a
+// partial; a fixed-order pass sums the partials (deterministic).
+#include "fna2_kernels.h"
+#include "fna2_tile.h"
+
+namespace fna2 {
+
+namespace {
+
+template <int D, int RPL>
+struct DqCfg {
+  static constexpr int NW = 4;
+  static constexpr int BM = kDqBM;  // queries per workgroup
+  static constexpr int BN = D == 128 ? 32 : kDqBN;  // keys per step (fits 2 waves/SIMD)
+  static constexpr int NKB = BN / 32;               // 32-key blocks per step
+  static constexpr int CD = D / 8;
+  static constexpr int CR = RPL > 0 ? RPL / 8 : 4;
+  static constexpr int KSD = D / 16;
+  static constexpr int KSR = RPL / 16;
+  static constexpr int NDB = D / 32;
+  static constexpr int NRB = RPL / 32;
+  static constexpr int KB = BN * D * 2;
+  static constexpr int RB = BN * RPL * 2;
+  static constexpr int VB = BN * D * 2;
+  static constexpr int STAGE = KB + RB + VB;
+};
+
+template <int D, int RPL>
+__device__ __forceinline__ void dq_body(const BwdParams& P) {
+  using C = DqCfg<D, RPL>;
+  __shared__ __attribute__((aligned(1024))) uint8_t st0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t st1[C::STAGE];
+  __shared__ float red[4];
+  const Problem& p = P.p;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = uni(tid >> 6);
+  const int l32 = lane & 31, hl = lane >> 5;
+  const int h = blockIdx.x % p.H;
+  const int tix = blockIdx.x / p.H;
+  int b, qt;
+  if (P.tiles_q) {
+    if (tix >= uni(*P.n_tiles_q)) {
+      if (tid == 0) P.dgs_partial[blockIdx.x] = 0.f;
+      return;
+    }
+    const int2 t = P.tiles_q[tix];
+    b = uni(t.x);
+    qt = uni(t.y);
+  } else {
+    const int nqt = cdiv(p.sq, C::BM);
+    b = tix % p.nseq;
+    qt = nqt - 1 - tix / p.nseq;
+  }
+  const SeqExt e = seq_ext_uniform(p, b);
+  const int kvh = h / p.group;
+  const bool graph = (RPL > 0) && (h < p.H_G);
+  const float bh = graph ? P.gs[h] / p.c : 0.f;
+  const int nrs = graph ? cdiv(p.R, 16) : 0;
+
+  const uint16_t* qb = seq_base<const uint16_t>(P.q, p, b, e.q0, h);
+  const uint16_t* ob = seq_base<const uint16_t>(P.dout, p, b, e.q0, h);
+  const uint16_t* kb = seq_base<const uint16_t>(P.k, p, b, e.k0, kvh);
+  const uint16_t* vb = seq_base<const uint16_t>(P.v, p, b, e.k0, kvh);
+  const uint16_t* rqb = graph ? seq_base<const uint16_t>(P.rq, p, b, e.q0, h) : qb;
+  const uint16_t* rkb = graph ? seq_base<const uint16_t>(P.rk, p, b, e.k0, h) : kb;
+
+  const int q0 = qt * C::BM;
+  const int qrow = q0 + wv * 32 + l32;
+  const bool qvalid = qrow < e.lq;
+  const int wq0 = q0 + wv * 32;
+  const int wq_last = min(wq0 + 31, e.lq - 1);
+  const int qrows = max(min(C::BM, e.lq - q0), 0);
+
+  // Stationary B operands: Qa and dO rows of this lane's query.
+  bf16x8 qreg[C::KSD + C::KSR];
+  bf16x8 oreg[C::KSD];
+  float lse2 = 0.f, dl = 0.f;
+  {
+    const uint32_t rb = (uint32_t)P.q.ss * 2u, orb = (uint32_t)P.dout.ss * 2u;
+    const auto rs = make_rsrc(qb + (int64_t)q0 * P.q.ss, (uint32_t)qrows * rb);
+    const auto ro = make_rsrc(ob + (int64_t)q0 * P.dout.ss, (uint32_t)qrows * orb);
+    const uint32_t vq = (uint32_t)(wv * 32 + l32) * rb + 16u * hl;
+    const uint32_t vo = (uint32_t)(wv * 32 + l32) * orb + 16u * hl;
+    const uint32_t qxor = p.qa < 0.f ? 0x80008000u : 0u;
+    const uint32_t qand = p.qa == 0.f ? 0u : 0xffffffffu;
+#pragma unroll
+    for (int s = 0; s < C::KSD; ++s) {
+      u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, vq + 32u * s, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = (v[i] & qand) ^ qxor;
+      qreg[s] = as_bf16x8(v);
+      oreg[s] = as_bf16x8(__builtin_amdgcn_raw_buffer_load_b128(ro, vo + 32u * s, 0, 0));
+    }
+    if constexpr (C::KSR > 0) {
+      const uint32_t rrb = (uint32_t)P.rq.ss * 2u;
+      const auto rr = make_rsrc(rqb + (int64_t)q0 * P.rq.ss, graph ? (uint32_t)qrows * rrb : 0u);
+      const uint32_t vr = (uint32_t)(wv * 32 + l32) * rrb + 16u * hl;
+#pragma unroll
+      for (int s = 0; s < C::KSR; ++s) {
+        const bool in = (2 * s + hl) * 8 < p.R;
+        u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rr, in ? vr + 32u * s : kOOB, 0, 0);
+        qreg[C::KSD + s] = as_bf16x8(scale_bf16x8(v, bh));
+      }
+    }
+    if (qvalid) {
+      lse2 = seq_base<const float>(P.lse, p, b, e.q0, h)[(int64_t)qrow * P.lse.ss] * kLog2e;
+      dl = seq_base<const float>(P.delta, p, b, e.q0, h)[(int64_t)qrow * P.delta.ss];
+    }
+  }
+
+  int kv_hi = e.lk;
+  if (p.causal) kv_hi = min(kv_hi, min(e.lq, q0 + C::BM));
+  const int nkb = cdiv(max(kv_hi, 0), C::BN);
+
+  const uint32_t krb = (uint32_t)P.k.ss * 2u, vrb = (uint32_t)P.v.ss * 2u;
+  const uint32_t rkrb = (uint32_t)P.rk.ss * 2u;
+  Dma<C::BN, C::CD, C::NW> dk, dv;
+  Dma<C::BN, C::CR, C::NW> dr;
+  dk.init(wv, lane, krb, C::CD);
+  dv.init(wv, lane, vrb, C::CD);
+  if constexpr (RPL > 0) dr.init(wv, lane, rkrb, p.R / 8);
+  auto issue = [&](int it, uint8_t* st) {
+    const int k0 = it * C::BN;
+    const uint32_t rows = (uint32_t)max(min(C::BN, e.lk - k0), 0);
+    dk.issue(make_rsrc(kb + (int64_t)k0 * P.k.ss, rows * krb), st, wv);
+    if constexpr (RPL > 0) {
+      if (graph) dr.issue(make_rsrc(rkb + (int64_t)k0 * P.rk.ss, rows * rkrb), st + C::KB, wv);
+    }
+    dv.issue(make_rsrc(vb + (int64_t)k0 * P.v.ss, rows * vrb), st + C::KB + C::RB, wv);
+  };
+
+  f32x16 acc[C::NDB + C::NRB];
+#pragma unroll
+  for (int i = 0; i < C::NDB + C::NRB; ++i) acc[i] = f32x16{};
+  const TrLane tl(lane);
+
+  auto step = [&](int it, const uint8_t* cur, uint8_t* nxt) {
+    wait_all_loads();
+    __syncthreads();
+    if (it + 1 < nkb) issue(it + 1, nxt);
+    __builtin_amdgcn_sched_barrier(0);
+    const int kbase = it * C::BN;
+    const bool active = (wq0 <= wq_last) && (!p.causal || kbase <= wq_last);
+    if (!active) return;
+    const uint8_t* kt = cur;
+    const uint8_t* rt = cur + C::KB;
+    const uint8_t* vt = cur + C::KB + C::RB;
+    bf16x8 db[C::NKB][2];
+#pragma unroll
+    for (int kb2 = 0; kb2 < C::NKB; ++kb2) {
+      const int row = kb2 * 32 + l32;
+      f32x16 sacc = f32x16{}, dpacc = f32x16{};
+#pragma unroll
+      for (int s = 0; s < C::KSD; ++s) sacc = mfma32(row_read<C::CD>(kt, row, 2 * s + hl), qreg[s], sacc);
+      if constexpr (C::KSR > 0) {
+#pragma unroll
+        for (int s = 0; s < C::KSR; ++s)
+          if (s < nrs) sacc = mfma32(row_read<C::CR>(rt, row, 2 * s + hl), qreg[C::KSD + s], sacc);
+      }
+#pragma unroll
+      for (int s = 0; s < C::KSD; ++s) dpacc = mfma32(row_read<C::CD>(vt, row, 2 * s + hl), oreg[s], dpacc);
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        u32x4 dk4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float dv2[2];
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int v = 8 * half + 2 * i + j;
+            const int key = kbase + kb2 * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
+            const bool ok = qvalid && key < e.lk && (!p.causal || key <= qrow);
+            const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[v], p.c2, -lse2));
+            dv2[j] = ok ? p.c * pr * (dpacc[v] - dl) : 0.f;
+          }
+          dk4[i] = pack_bf16(dv2[0], dv2[1]);
+        }
+        db[kb2][half] = as_bf16x8(dk4);
+      }
+    }
+    // dQa^T += Ka^T dA^T
+#pragma unroll
+    for (int kb2 = 0; kb2 < C::NKB; ++kb2)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int k0 = kb2 * 32 + 16 * half;
+#pragma unroll
+        for (int f = 0; f < C::NDB; ++f)
+          acc[f] = mfma32(tr_operand<C::CD>(kt, tl, k0, 32 * f), db[kb2][half], acc[f]);
+        if constexpr (C::NRB > 0) {
+          if (graph) {
+#pragma unroll
+            for (int f = 0; f < C::NRB; ++f)
+              acc[C::NDB + f] =
+                  mfma32(tr_operand<C::CR>(rt, tl, k0, 32 * f), db[kb2][half], acc[C::NDB + f]);
+          }
+        }
+      }
+  };
+
+  if (nkb > 0) issue(0, st0);
+  for (int it = 0; it < nkb; it += 2) {
+    step(it, st0, st1);
+    if (it + 1 < nkb) step(it + 1, st1, st0);
+  }
+
+  float gpart = 0.f;
+  if (qvalid) {
+    uint16_t* drow = seq_base<uint16_t>(P.dq, p, b, e.q0, h) + (int64_t)qrow * P.dq.ss;
+#pragma unroll
+    for (int d = 0; d < C::NDB; ++d)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        u32x2 val;
+        val[0] = pack_bf16(p.qa * acc[d][4 * g], p.qa * acc[d][4 * g + 1]);
+        val[1] = pack_bf16(p.qa * acc[d][4 * g + 2], p.qa * acc[d][4 * g + 3]);
+        *(u32x2*)(drow + d * 32 + 8 * g + 4 * hl) = val;
+      }
+    if constexpr (C::NRB > 0) {
+      if (graph) {
+        uint16_t* rrow = seq_base<uint16_t>(P.drq, p, b, e.q0, h) + (int64_t)qrow * P.drq.ss;
+        const uint16_t* rq = rqb + (int64_t)qrow * P.rq.ss;
+#pragma unroll
+        for (int f = 0; f < C::NRB; ++f)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int rf = f * 32 + 8 * g + 4 * hl;
+            if (rf < p.R) {
+              const f32x16& a = acc[C::NDB + f];
+              const u32x2 rv = *(const u32x2*)(rq + rf);
+              gpart += bf16_lo(rv[0]) * a[4 * g] + bf16_hi(rv[0]) * a[4 * g + 1] +
+                       bf16_lo(rv[1]) * a[4 * g + 2] + bf16_hi(rv[1]) * a[4 * g + 3];
+              u32x2 val;
+              val[0] = pack_bf16(bh * a[4 * g], bh * a[4 * g + 1]);
+              val[1] = pack_bf16(bh * a[4 * g + 2], bh * a[4 * g + 3]);
+              *(u32x2*)(rrow + rf) = val;
+            }
+          }
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) gpart += __shfl_xor(gpart, off);
+  if (lane == 0) red[wv] = gpart;
+  __syncthreads();
+  if (tid == 0) P.dgs_partial[blockIdx.x] = ((red[0] + red[1]) + (red[2] + red[3])) / p.c;
+}
+
+// WAVES: waves per SIMD the register budget is cut for (d128/r64 needs more
+// registers than two waves allow without spilling).
+#define FNA2_DQ_KERNEL(D, RPL, WAVES)                                                   \
+  __global__ __launch_bounds__(256, WAVES) void dq_kernel_d##D##_r##RPL(const BwdParams P) { \
+    dq_body<D, RPL>(P);                                                                 \
+  }
+FNA2_DQ_KERNEL(64, 0, 2)
+FNA2_DQ_KERNEL(64, 32, 2)
+FNA2_DQ_KERNEL(64, 64, 2)
+FNA2_DQ_KERNEL(128, 0, 2)
+FNA2_DQ_KERNEL(128, 32, 2)
+FNA2_DQ_KERNEL(128, 64, 1)
+#undef FNA2_DQ_KERNEL
+
+}  // namespace
+
+hipError_t launch_bwd_dq(const BwdParams& P, int rpl, int grid, hipStream_t s) {
+  if (grid <= 0) return hipSuccess;
+  void (*k)(const BwdParams) = nullptr;
+  if (P.p.D == 64) k = rpl == 0 ? dq_kernel_d64_r0 : rpl == 32 ? dq_kernel_d64_r32 : dq_kernel_d64_r64;
+  if (P.p.D == 128)
+    k = rpl == 0 ? dq_kernel_d128_r0 : rpl == 32 ? dq_kernel_d128_r32 : dq_kernel_d128_r64;
+  if (!k || (rpl != 0 && rpl != 32 && rpl != 64)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k, dim3(grid), dim3(256), 0, s, P);
+  return hipGetLastError();
+}
+
+}  // namespace fna2

@@ -39,7 +39,10 @@ struct FwdCfg {
 template <int D, int RPL>
 __device__ __forceinline__ void fwd_body(const FwdParams& P) {
   using C = FwdCfg<D, RPL>;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * C::STAGE];
+  // Two stages as separate objects: the compiler can then tell that reads of
+  // one stage never alias the DMA into the other and does not wait for it.
+  __shared__ __attribute__((aligned(1024))) uint8_t stage0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t stage1[C::STAGE];
   const Problem& p = P.p;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
@@ -120,10 +123,9 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
     if (graph) rkb = seq_base<const uint16_t>(P.rk, p, b, e.k0, h);
     dr.init(wv, lane, rkrb, p.R / 8);
   }
-  auto issue = [&](int kt, int stage) {
+  auto issue = [&](int kt, uint8_t* base) {
     const int k0 = kt * C::BN;
     const uint32_t rows = (uint32_t)max(min(C::BN, e.lk - k0), 0);
-    uint8_t* base = smem + stage * C::STAGE;
     dk.issue(make_rsrc(kb + (int64_t)k0 * P.k.ss, rows * krb), base, wv);
     if constexpr (C::CR > 0) {
       if (graph) dr.issue(make_rsrc(rkb + (int64_t)k0 * P.rk.ss, rows * rkrb), base + C::KBYTES, wv);
@@ -137,18 +139,19 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
   float m_i = kNegInf, l_i = 0.f;
   const TrLane tl(lane);
 
-  if (nkv > 0) issue(0, 0);
-  for (int kt = 0; kt < nkv; ++kt) {
+  // One key tile: wait for its DMA, start the next one into the other stage,
+  // then compute on this one.
+  auto step = [&](int kt, const uint8_t* cur, uint8_t* nxt) {
     wait_all_loads();
     __syncthreads();
-    if (kt + 1 < nkv) issue(kt + 1, (kt + 1) & 1);
+    if (kt + 1 < nkv) issue(kt + 1, nxt);
+    __builtin_amdgcn_sched_barrier(0);  // keep the whole prefetch ahead of the compute
     const int kbase = kt * C::BN;
     const bool active = (wq0 <= wq_last) && (!p.causal || kbase <= wq_last);
-    if (!active) continue;
-    const uint8_t* kl = smem + (kt & 1) * C::STAGE;
+    if (!active) return;
+    const uint8_t* kl = cur;
     const uint8_t* rl = kl + C::KBYTES;
     const uint8_t* vl = rl + C::RBYTES;
-
     // S^T = Ka Qa^T for two 32-key blocks.
     f32x16 sacc[C::BN / 32];
 #pragma unroll
@@ -211,6 +214,12 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
 #pragma unroll
       for (int d = 0; d < D / 32; ++d)
         oacc[d] = mfma32(tr_operand<C::CD>(vl, tl, 16 * s, 32 * d), pb[s], oacc[d]);
+  };
+
+  if (nkv > 0) issue(0, stage0);
+  for (int kt = 0; kt < nkv; kt += 2) {
+    step(kt, stage0, stage1);
+    if (kt + 1 < nkv) step(kt + 1, stage1, stage0);
   }
 
   const float l_tot = wave_pair_sum(l_i);

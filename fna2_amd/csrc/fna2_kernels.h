@@ -16,6 +16,7 @@ struct FwdParams {
 struct BwdParams {
   Problem p;
   TView q, k, v, rq, rk, o, lse, dout, delta, dq, dk, dv, drq, drk;
+  TView rqs;             // workspace: bf16(graph_scale / c * Rq), [rows][H_G][rank width]
   const float* gs;
   float* dgs;            // [H_G]
   float* dgs_partial;    // [dq grid] per-workgroup partial sums of d_gs
@@ -31,15 +32,9 @@ constexpr int kFwdBN = 64;
 // Backward: dK/dV kernel tiles keys by kKvBN and walks queries kKvBM at a
 // time; the dQ kernel tiles queries by kDqBM and walks keys kDqBN at a time.
 constexpr int kKvBN = 128;
-constexpr int kKvBM = 32;
+constexpr int kKvBM = 64;
 constexpr int kDqBM = 128;
-constexpr int kDqBN = 32;
-
-// Padded rank used by the kernels: 0 without graph heads, else R rounded up
-// to a multiple of 16.
-inline int padded_rank(int H_G, int R) {
-  return (H_G > 0 && R > 0) ? ((R + 15) / 16) * 16 : 0;
-}
+constexpr int kDqBN = 64;
 
 // Rank padded to a multiple of 32 (the LDS tile width of the rank part of a
 // key or query tile): 0, 32 or 64.
@@ -48,9 +43,9 @@ inline int padded_rank32(int H_G, int R) {
 }
 
 hipError_t launch_fwd(const FwdParams& P, int rp, int grid, hipStream_t s);
-hipError_t launch_bwd_delta(const BwdParams& P, hipStream_t s);
-hipError_t launch_bwd_dkdv(const BwdParams& P, int rp, int grid, hipStream_t s);
-hipError_t launch_bwd_dq(const BwdParams& P, int rp, int grid, hipStream_t s);
+hipError_t launch_bwd_prep(const BwdParams& P, int rpl, hipStream_t s);
+hipError_t launch_bwd_dkdv(const BwdParams& P, int rpl, int grid, hipStream_t s);
+hipError_t launch_bwd_dq(const BwdParams& P, int rpl, int grid, hipStream_t s);
 hipError_t launch_bwd_dgs(const BwdParams& P, int nparts, hipStream_t s);
 
 }  // namespace fna2
