@@ -1,0 +1,309 @@
+"""Pins the CPU oracle (oracle/fna2_oracle.py) without trusting its own formulas.
+
+Checks, each chosen so that a plausible mistake in the oracle fails at least
+one of them (the mutation tests at the end plant such mistakes):
+  * a pure-Python brute force on tiny inputs (independent loops);
+  * torch's scaled_dot_product_attention, a library routine: is_causal=True
+    when graph_scale = 0, an explicit float mask built with torch otherwise;
+  * torch autograd through that SDPA formulation (fp64, eps = 0);
+  * central finite differences of the oracle's own forward;
+  * identities: O_0 = V_0 (causal), key-permutation invariance (non-causal),
+    <Q, dQ> = <K, dK> and gs * d_gs = <Rq, dRq> = <Rk, dRk> per head,
+    sum_j dK_j = 0, sum_j dV_j = sum_i dO_i;
+  * varlen == per-sequence dense;
+  * c1 (fp32) within 1e-4 max abs of fp64;
+  * the reference's eager path restated in oracle/eager_reference.py
+    (bias rounded to bf16, SDPA) within the reference's own 0.05 tolerance.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import eager_reference as ER
+from oracle import fna2_oracle as O
+
+
+def rnd(shape, seed, std=1.0):
+    return np.random.default_rng(seed).standard_normal(shape) * std
+
+
+def brute_force(q, k, v, rq, rk, gs, scale, causal, eps=O.EPS):
+    """Triple loops over (b, h, i); q [B,H,S,D], k/v [B,HKV,Sk,D], r [B,HG,S,R]."""
+    B, H, S, D = q.shape
+    HKV, Sk = k.shape[1], k.shape[2]
+    HG = 0 if rq is None else rq.shape[1]
+    out = np.zeros_like(q)
+    lse = np.full((B, H, S), -np.inf)
+    for b in range(B):
+        for h in range(H):
+            kv = h // (H // HKV)
+            for i in range(S):
+                scores = []
+                for j in range(Sk):
+                    if causal and j > i:
+                        continue
+                    s = scale * sum(q[b, h, i, d] * k[b, kv, j, d] for d in range(D))
+                    if h < HG:
+                        s += gs[h] * sum(rq[b, h, i, r] * rk[b, h, j, r] for r in range(rq.shape[3]))
+                    scores.append((j, s))
+                if not scores:
+                    continue
+                m = max(s for _, s in scores)
+                l = sum(math.exp(s - m) for _, s in scores)
+                for j, s in scores:
+                    out[b, h, i] += math.exp(s - m) * v[b, kv, j] / (l + eps)
+                lse[b, h, i] = m + math.log(l + eps)
+    return out, lse
+
+
+def make(B=1, H=2, S=7, D=4, HKV=1, HG=1, R=3, Sk=None, seed=0, gs_val=None):
+    Sk = S if Sk is None else Sk
+    q = rnd((B, H, S, D), seed)
+    k = rnd((B, HKV, Sk, D), seed + 1)
+    v = rnd((B, HKV, Sk, D), seed + 2)
+    rq = rnd((B, HG, S, R), seed + 3, 0.5) if HG else None
+    rk = rnd((B, HG, Sk, R), seed + 4, 0.5) if HG else None
+    gs = rnd((HG,), seed + 5) if gs_val is None else np.full((HG,), gs_val)
+    dout = rnd((B, H, S, D), seed + 6)
+    return q, k, v, rq, rk, gs, dout
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", [dict(), dict(H=4, HKV=2, HG=3, R=2, S=6, Sk=9),
+                                   dict(B=2, H=2, HKV=2, HG=0, R=0, S=5)])
+def test_forward_matches_brute_force(causal, shape):
+    q, k, v, rq, rk, gs, _ = make(**shape, seed=3)
+    scale = 0.7
+    o, l = O.forward(q, k, v, rq, rk, gs, scale, causal)
+    bo, bl = brute_force(q, k, v, rq, rk, gs, scale, causal)
+    np.testing.assert_allclose(o, bo, atol=1e-12)
+    np.testing.assert_allclose(l, bl, atol=1e-12)
+
+
+def _sdpa_torch(q, k, v, rq, rk, gs, scale, causal, eps_free=True):
+    """fp64 torch SDPA with an explicit additive mask (autograd-able)."""
+    B, H, S, D = q.shape
+    HKV, Sk = k.shape[1], k.shape[2]
+    G = H // HKV
+    ke, ve = k.repeat_interleave(G, 1), v.repeat_interleave(G, 1)
+    bias = torch.zeros(B, H, S, Sk, dtype=torch.float64)
+    if rq is not None and rq.shape[1]:
+        HG = rq.shape[1]
+        bias = torch.cat([gs.view(1, HG, 1, 1) * (rq @ rk.transpose(-1, -2)),
+                          torch.zeros(B, H - HG, S, Sk, dtype=torch.float64)], 1)
+    if causal:
+        keep = torch.ones(S, Sk, dtype=torch.bool).tril()
+        bias = bias.masked_fill(~keep, float("-inf"))
+    return F.scaled_dot_product_attention(q, ke, ve, attn_mask=bias, scale=scale)
+
+
+def test_forward_matches_torch_sdpa_gs_zero():
+    q, k, v, rq, rk, gs, _ = make(B=2, H=4, S=33, D=8, HKV=2, HG=2, R=4, gs_val=0.0, seed=5)
+    o, _ = O.forward(q, k, v, rq, rk, gs, 0.3, True, eps=0.0)
+    t = lambda x: torch.tensor(x)
+    ref = F.scaled_dot_product_attention(t(q), t(k).repeat_interleave(2, 1),
+                                         t(v).repeat_interleave(2, 1), is_causal=True, scale=0.3)
+    np.testing.assert_allclose(o, ref.numpy(), atol=1e-12)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_forward_matches_torch_sdpa_bias(causal):
+    q, k, v, rq, rk, gs, _ = make(B=2, H=4, S=17, D=8, HKV=2, HG=3, R=5, seed=6)
+    o, _ = O.forward(q, k, v, rq, rk, gs, 0.35, causal, eps=0.0)
+    t = lambda x: torch.tensor(x)
+    ref = _sdpa_torch(t(q), t(k), t(v), t(rq), t(rk), t(gs), 0.35, causal)
+    np.testing.assert_allclose(o, ref.numpy(), atol=1e-12)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_backward_matches_torch_autograd(causal):
+    q, k, v, rq, rk, gs, dout = make(B=2, H=4, S=11, D=6, HKV=2, HG=3, R=4, Sk=None, seed=7)
+    scale = 0.41
+    o, l = O.forward(q, k, v, rq, rk, gs, scale, causal, eps=0.0)
+    got = O.backward(dout, q, k, v, rq, rk, gs, o, l, scale, causal)
+    leaves = [torch.tensor(x, requires_grad=True) for x in (q, k, v, rq, rk, gs)]
+    out = _sdpa_torch(*leaves, scale, causal)
+    ref = torch.autograd.grad(out, leaves, torch.tensor(dout))
+    for g, r in zip(got, ref):
+        np.testing.assert_allclose(g, r.numpy(), atol=1e-10)
+
+
+def test_backward_matches_finite_differences():
+    q, k, v, rq, rk, gs, dout = make(B=1, H=2, S=5, D=3, HKV=1, HG=2, R=2, seed=8)
+    scale, causal = 0.6, True
+    o, l = O.forward(q, k, v, rq, rk, gs, scale, causal, eps=0.0)
+    grads = O.backward(dout, q, k, v, rq, rk, gs, o, l, scale, causal)
+    args = [q, k, v, rq, rk, gs]
+
+    def loss(a):
+        return float(np.sum(dout * O.forward(*a, scale, causal, eps=0.0)[0]))
+
+    rng = np.random.default_rng(0)
+    for idx in range(6):
+        u = rng.standard_normal(args[idx].shape)
+        h = 1e-6
+        ap = [a.copy() for a in args]
+        am = [a.copy() for a in args]
+        ap[idx] = ap[idx] + h * u
+        am[idx] = am[idx] - h * u
+        fd = (loss(ap) - loss(am)) / (2 * h)
+        an = float(np.sum(grads[idx] * u))
+        assert abs(fd - an) < 1e-6 * max(1.0, abs(an)), (idx, fd, an)
+
+
+def test_identities():
+    q, k, v, rq, rk, gs, dout = make(B=1, H=3, S=40, D=8, HKV=3, HG=2, R=4, seed=9)
+    scale = 0.3
+    o, l = O.forward(q, k, v, rq, rk, gs, scale, True)
+    np.testing.assert_allclose(o[:, :, 0], v[:, :, 0] / (1 + O.EPS), atol=1e-12)  # O_0 = V_0
+    # exact identities hold without the 1e-6 normaliser (they are off by ~delta * 1e-6 with it)
+    o, l = O.forward(q, k, v, rq, rk, gs, scale, True, eps=0.0)
+    dq, dk, dv, drq, drk, dgs = O.backward(dout, q, k, v, rq, rk, gs, o, l, scale, True)
+    for h in range(3):
+        a, b = np.sum(q[0, h] * dq[0, h]), np.sum(k[0, h] * dk[0, h])
+        assert abs(a - b) < 1e-9 * max(1, abs(a))
+        np.testing.assert_allclose(dk[0, h].sum(0), 0, atol=1e-9)
+        np.testing.assert_allclose(dv[0, h].sum(0), dout[0, h].sum(0), atol=1e-9)
+    for h in range(2):
+        x, y, z = gs[h] * dgs[h], np.sum(rq[0, h] * drq[0, h]), np.sum(rk[0, h] * drk[0, h])
+        assert abs(x - y) < 1e-9 * max(1, abs(x)) and abs(x - z) < 1e-9 * max(1, abs(x))
+
+
+def test_noncausal_key_permutation_invariance():
+    q, k, v, rq, rk, gs, _ = make(B=1, H=2, S=9, D=5, HKV=2, HG=2, R=3, seed=10)
+    o, _ = O.forward(q, k, v, rq, rk, gs, 0.5, False)
+    perm = np.random.default_rng(1).permutation(9)
+    o2, _ = O.forward(q, k[:, :, perm], v[:, :, perm], rq, rk[:, :, perm], gs, 0.5, False)
+    np.testing.assert_allclose(o, o2, atol=1e-12)
+
+
+def test_varlen_equals_per_sequence_dense():
+    lengths = [3, 0, 7, 1, 5]
+    H, D, HKV, HG, R = 4, 6, 2, 3, 4
+    T = sum(lengths)
+    rng = np.random.default_rng(2)
+    q, k, v, dout = (rng.standard_normal((T, n, D)) for n in (H, HKV, HKV, H))
+    rq, rk = rng.standard_normal((T, HG, R)), rng.standard_normal((T, HG, R))
+    gs = rng.standard_normal(HG)
+    cu = np.concatenate([[0], np.cumsum(lengths)])
+    for causal in (True, False):
+        o, l = O.forward(q, k, v, rq, rk, gs, 0.4, causal, cu, cu)
+        g = O.backward(dout, q, k, v, rq, rk, gs, o, l, 0.4, causal, cu, cu)
+        dgs = np.zeros(HG)
+        for b in range(len(lengths)):
+            s0, s1 = cu[b], cu[b + 1]
+            t4 = lambda x: x[s0:s1].transpose(1, 0, 2)[None]
+            od, ld = O.forward(t4(q), t4(k), t4(v), t4(rq), t4(rk), gs, 0.4, causal)
+            gd = O.backward(t4(dout), t4(q), t4(k), t4(v), t4(rq), t4(rk), gs, od, ld, 0.4, causal)
+            np.testing.assert_allclose(o[s0:s1], od[0].transpose(1, 0, 2), atol=1e-12)
+            for gv, gdd in zip(g[:5], gd[:5]):
+                np.testing.assert_allclose(gv[s0:s1], gdd[0].transpose(1, 0, 2), atol=1e-12)
+            dgs += gd[5]
+        np.testing.assert_allclose(g[5], dgs, atol=1e-12)
+
+
+def test_c1_fp32_within_1e4_of_fp64():
+    """Config c1: dense causal forward, fp32, B2 H4 L256 d64 r8 (CPU oracle only)."""
+    from fna2_amd import configs
+    cfg = configs.get("c1")
+    inp = configs.make_inputs(cfg, with_dout=False)
+    o32, _ = O.forward(inp.q, inp.k, inp.v, inp.r_q, inp.r_k, inp.graph_scale, inp.scale, True,
+                       dtype=np.float32)
+    o64, _ = O.forward(inp.q, inp.k, inp.v, inp.r_q, inp.r_k, inp.graph_scale, inp.scale, True)
+    assert np.max(np.abs(o32 - o64)) < 1e-4
+
+
+def test_eager_reference_restatement_exact_in_fp64():
+    """The restated eager path (validate_fna2.py:84-112) run on fp64 inputs rounds only
+    its bias, which it builds in fp32 as the reference does (:97, rq.float()): it
+    must equal the oracle to fp32 bias rounding.  Pins the restatement's
+    bias/GQA/vanilla-pad/mask construction."""
+    q, k, v, rq, rk, gs, _ = make(B=2, H=8, S=24, D=8, HKV=4, HG=4, R=6, seed=12)
+    t = lambda x: torch.tensor(x)
+    for causal in (True, False):
+        out = ER.sdpa_reference(t(q), t(k), t(v), t(rq), t(rk), t(gs), 0.3, causal)
+        ref, _ = O.forward(q, k, v, rq, rk, gs, 0.3, causal, eps=0.0)
+        np.testing.assert_allclose(out.numpy(), ref, atol=1e-6)
+    lengths = [5, 9, 1]
+    cu = torch.tensor([0, 5, 14, 15])
+    T = 15
+    qv, kv, vv = t(rnd((T, 4, 8), 1)), t(rnd((T, 2, 8), 2)), t(rnd((T, 2, 8), 3))
+    rqv, rkv, gv = t(rnd((T, 3, 4), 4)), t(rnd((T, 3, 4), 5)), t(rnd((3,), 6))
+    outv = ER.sdpa_reference_varlen(qv, kv, vv, rqv, rkv, gv, cu, cu, 0.3, True)
+    refv, _ = O.forward(qv, kv, vv, rqv, rkv, gv, 0.3, True, cu.numpy(), cu.numpy(), eps=0.0)
+    np.testing.assert_allclose(outv.numpy(), refv, atol=1e-6)
+
+
+def test_eager_reference_bf16_within_reference_tolerance():
+    """In bf16 the eager path rounds the bias to bf16 (validate_fna2.py:102); at the
+    configs' R scale (std 1/sqrt(R)) it stays within the reference's 0.05 (:59)."""
+    g = torch.Generator().manual_seed(42)
+    mk = lambda *s, std=1.0: (torch.randn(*s, generator=g) * std).bfloat16()
+    q, k, v = mk(2, 8, 128, 64), mk(2, 4, 128, 64), mk(2, 4, 128, 64)
+    rq, rk = mk(2, 4, 128, 32, std=32 ** -0.5), mk(2, 4, 128, 32, std=32 ** -0.5)
+    gs = torch.randn(4, generator=g)
+    out = ER.sdpa_reference(q, k, v, rq, rk, gs, 0.125, causal=True)
+    ref, _ = O.forward(q, k, v, rq, rk, gs, 0.125, True)
+    assert np.max(np.abs(out.double().numpy() - ref)) < 0.05
+
+
+def test_flops_formula():
+    fwd, bwd = O.flops([(256, 256)] * 2, H=4, D=64, R=8, causal=True)
+    pairs = 2 * 256 * 257 // 2
+    assert fwd == pairs * 4 * (4 * 64 + 2 * 8) and bwd == pairs * 4 * (10 * 64 + 6 * 8)
+
+
+# ── planted mistakes: each must make at least one pinning check fail ──────────
+
+def _run_pins():
+    """The pinning checks above, on fresh inputs; raises if any fails."""
+    test_forward_matches_brute_force(True, dict(H=4, HKV=2, HG=3, R=2, S=6, Sk=9))
+    test_forward_matches_torch_sdpa_bias(True)
+    test_forward_matches_torch_sdpa_bias(False)
+    test_backward_matches_torch_autograd(True)
+    test_identities()
+
+
+@pytest.mark.parametrize("mutation", ["drop_bias", "causal_off_by_one", "transposed_bias",
+                                      "drop_gs_in_drk", "wrong_kv_head"])
+def test_planted_mistakes_are_caught(monkeypatch, mutation):
+    if mutation == "drop_bias":
+        monkeypatch.setattr(O, "_scores", lambda Qb, K, Rqb, Rk, g, scale: scale * (Qb @ K.T))
+    elif mutation == "causal_off_by_one":
+        def bad_mask(i0, nq, lk, causal):
+            qi = np.arange(i0, i0 + nq)[:, None]
+            kj = np.arange(lk)[None, :]
+            return (kj < qi) | (kj == 0) if causal else np.ones((nq, lk), bool)
+        monkeypatch.setattr(O, "_mask", bad_mask)
+    elif mutation == "transposed_bias":
+        def bad_scores(Qb, K, Rqb, Rk, g, scale):
+            S = scale * (Qb @ K.T)
+            if Rqb is not None:
+                n = min(S.shape)
+                B = g * (Rqb @ Rk.T)
+                B[:n, :n] = B[:n, :n].T
+                S = S + B
+            return S
+        monkeypatch.setattr(O, "_scores", bad_scores)
+    elif mutation == "drop_gs_in_drk":
+        orig = O.head_backward
+
+        def bad_backward(dO, Q, K, V, Rq, Rk, g, scale, causal, Ov, lse):
+            res = list(orig(dO, Q, K, V, Rq, Rk, g, scale, causal, Ov, lse))
+            if Rk is not None and g != 0:
+                res[4] = res[4] / g
+            return tuple(res)
+        monkeypatch.setattr(O, "head_backward", bad_backward)
+    elif mutation == "wrong_kv_head":
+        orig_fwd = O.head_forward
+        calls = {"n": 0}
+
+        def bad_fwd(Q, K, V, *a, **kw):
+            calls["n"] += 1
+            return orig_fwd(Q, K * (1.0 + 0.01 * (calls["n"] % 2)), V, *a, **kw)
+        monkeypatch.setattr(O, "head_forward", bad_fwd)
+    with pytest.raises(AssertionError):
+        _run_pins()
