@@ -60,12 +60,10 @@ def kernel_bytes(cfg, name):
     lse = row(H, 1, 4)
     if name == "fwd":   # read Q K V Rq Rk, write O LSE
         return q + 2 * kv + 2 * r + q + lse
-    if name == "delta":  # read O dO, write delta
-        return 2 * q + lse
     if name == "dkdv":  # read Q K V dO Rq Rk LSE delta, write dK dV dRk
         return q + 2 * kv + q + 2 * r + 2 * lse + 2 * kv + r
-    if name == "dq":    # read Q K V dO Rq Rk LSE delta, write dQ dRq
-        return q + 2 * kv + q + 2 * r + 2 * lse + q + r
+    if name == "dq":    # read Q K V O dO Rq Rk LSE, write dQ dRq delta
+        return q + 2 * kv + 2 * q + 2 * r + 2 * lse + q + r
     raise KeyError(name)
 
 
@@ -74,7 +72,7 @@ def kernel_flops(cfg, name):
     dRk); dQ kernel 2d+2r (dQ, dRq) per visible pair per head (sum = bwd 10d+6r)."""
     pairs = sum(n * (n + 1) // 2 if cfg.causal else n * n for n in cfg.seq_lengths()) * cfg.H
     per = {"fwd": 4 * cfg.D + 2 * cfg.R, "dkdv": 8 * cfg.D + 4 * cfg.R,
-           "dq": 2 * cfg.D + 2 * cfg.R, "delta": 0}[name]
+           "dq": 2 * cfg.D + 2 * cfg.R}[name]
     return pairs * per
 
 

@@ -86,7 +86,7 @@ class FwdArgs(ctypes.Structure):
 
 
 FWD_EVENTS = 2
-BWD_EVENTS = 6
+BWD_EVENTS = 4
 
 
 class BwdArgs(ctypes.Structure):

@@ -8,16 +8,17 @@
 // of S = Qa Ka^T and dP = dO V^T, one key per lane).  The workgroup walks
 // the query heads of its GQA group and, for each, the 64-query blocks that
 // can see its keys (causal: from the key tile's diagonal on).  Per block:
-//   S, dP      (64 x 32 per wave)       A operands: Q | Rq' and dO rows (LDS)
-//   P  = exp(S - LSE),  dA = c P (dP - delta)
+//   S, dP      (64 x 32 per wave)       A operands: Q | bf16(b Rq) and dO rows
+//   P  = exp(S - LSE),  dS = P (dP - delta)
 //   dV^T  += dO^T P                    A operand: dO^T by transpose reads
-//   dKa^T += [Q | Rq']^T dA = [dK / a | dRk]^T  A operand: (Q | Rq')^T by
-//                                               transpose reads
-// with Rq' = bf16(graph_scale / c * Rq) written by the backward pre-pass and
-// the sign/zero factor a of the augmented query carried by the stationary K
-// (exact), so the recomputed S equals the forward's bit for bit.
+//   acc^T += [Q | Rq]^T dS             A operand: (Q | Rq)^T by transpose reads
+// and the epilogue writes dK = a c acc_D, dRk = b c acc_R (b c = graph_scale).
+// The rank part of the score operand is rounded as bf16(b Rq) from the raw
+// Rq tile, as the forward does, and the sign/zero factor a of the augmented
+// query rides on the stationary K (exact), so the recomputed S equals the
+// forward's bit for bit.
 // dK and dV accumulate over the whole GQA group in fp32 registers: no atomics.
-// Q, Rq', dO, LSE and delta tiles stream in by DMA through a three-stage ring
+// Q, Rq, dO, LSE and delta tiles stream in by DMA through a three-stage ring
 // of separate LDS objects (the loop is unrolled by three so that the compiler
 // can prove reads and in-flight DMA never alias).
 #include "fna2_kernels.h"
@@ -141,12 +142,12 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
 
   // DMA plans for the streamed tiles.
   const uint32_t qrb = (uint32_t)P.q.ss * 2u, orb = (uint32_t)P.dout.ss * 2u;
-  const uint32_t srb = (uint32_t)P.rqs.ss * 2u;
+  const uint32_t srb = (uint32_t)P.rq.ss * 2u;
   Dma<C::BM, C::CD, C::NW> dmq, dmo;
   Dma<C::BM, C::CR, C::NW> dmr;
   dmq.init(wv, lane, qrb, C::CD);
   dmo.init(wv, lane, orb, C::CD);
-  if constexpr (RPL > 0) dmr.init(wv, lane, srb, C::CR);
+  if constexpr (RPL > 0) dmr.init(wv, lane, srb, p.R / 8);
   const uint32_t lrb = (uint32_t)P.lse.ss * 4u, drb = (uint32_t)P.delta.ss * 4u;
   const bool is_delta = (wv & 1) != 0;                 // waves 1, 3 load delta
   const int lslot = (wv & 1) * C::BM * 4 + (wv >> 1) * 2 * C::BM * 4;  // 2, 3: scratch rows
@@ -163,8 +164,8 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     dmq.issue(make_rsrc(qb + (int64_t)qbase * P.q.ss, rows * qrb), st, wv);
     if constexpr (RPL > 0) {
       const bool graph = h < p.H_G;
-      const uint16_t* sb = graph ? seq_base<const uint16_t>(P.rqs, p, b, e.q0, h) : qb;
-      dmr.issue(make_rsrc(sb + (int64_t)qbase * P.rqs.ss, graph ? rows * srb : 0u), st + C::QB,
+      const uint16_t* sb = graph ? seq_base<const uint16_t>(P.rq, p, b, e.q0, h) : qb;
+      dmr.issue(make_rsrc(sb + (int64_t)qbase * P.rq.ss, graph ? rows * srb : 0u), st + C::QB,
                 wv);
     }
     dmo.issue(make_rsrc(ob + (int64_t)qbase * P.dout.ss, rows * orb), st + C::QB + C::RB, wv);
@@ -179,6 +180,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
   auto write_drk = [&](int h) {
     if constexpr (C::NRB > 0) {
       if (h < p.H_G && kvalid) {
+        const float sr = P.gs[h];  // dRk = b c acc_R with b c = graph_scale
         uint16_t* rrow = seq_base<uint16_t>(P.drk, p, b, e.k0, h) + (int64_t)key * P.drk.ss;
 #pragma unroll
         for (int f = 0; f < C::NRB; ++f)
@@ -188,8 +190,8 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
             if (rf < p.R) {
               const f32x16& a = dkacc[C::NDB + f];
               u32x2 val;
-              val[0] = pack_bf16(a[4 * g], a[4 * g + 1]);
-              val[1] = pack_bf16(a[4 * g + 2], a[4 * g + 3]);
+              val[0] = pack_bf16(sr * a[4 * g], sr * a[4 * g + 1]);
+              val[1] = pack_bf16(sr * a[4 * g + 2], sr * a[4 * g + 3]);
               *(u32x2*)(rrow + rf) = val;
             }
           }
@@ -209,6 +211,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     const int qi = it - hi * nqb;
     const int h = kvh * p.group + hi;
     const bool graph = (RPL > 0) && (h < p.H_G);
+    const float bh = graph ? P.gs[h] / p.c : 0.f;
     if (qi == 0 && it > 0) {  // next head of the GQA group
       load_rk(h);
 #pragma unroll
@@ -216,6 +219,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     }
     const int qbase = (qb_lo + qi) * C::BM;
     const bool active = wave_keys && (!p.causal || qbase + C::BM - 1 >= wk0);
+    const bool diag = p.causal && wk0 + 31 > qbase;
     if (active) {
       const uint8_t* qt = cur;
       const uint8_t* rt = cur + C::QB;
@@ -232,11 +236,23 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
         if constexpr (C::KSR > 0) {
 #pragma unroll
           for (int s = 0; s < C::KSR; ++s)
-            if (s < nrs) sacc = mfma32(row_read<C::CR>(rt, row, 2 * s + hl), kreg[C::KSD + s], sacc);
+            if (s < nrs)
+              sacc = mfma32(as_bf16x8(scale_bf16x8(as_u32x4(row_read<C::CR>(rt, row, 2 * s + hl)), bh)),
+                            kreg[C::KSD + s], sacc);
         }
 #pragma unroll
         for (int s = 0; s < C::KSD; ++s) dpacc = mfma32(row_read<C::CD>(ot, row, 2 * s + hl), vreg[s], dpacc);
-        // P and dA for rows rb*32 + 8g + 4hl + j (accumulator register 4g + j).
+        // P and dS for rows rb*32 + 8g + 4hl + j (accumulator register 4g + j).
+        // Zero-filled query rows (past the sequence) have Q = dO = LSE =
+        // delta = 0 and so P (dP - delta) = 0: only the causal diagonal needs
+        // a mask; columns of keys past the sequence are never stored.
+        if (diag) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int q = qbase + rb * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
+            sacc[v] = key <= q ? sacc[v] : kNegInf;
+          }
+        }
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
           u32x4 pk, dk;
@@ -250,12 +266,8 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               const int v = 4 * g + j;
-              const int q = qbase + r0 + j;
-              const bool ok = q < e.lq && kvalid && (!p.causal || key <= q);
-              const float pr = __builtin_amdgcn_exp2f(
-                  __builtin_fmaf(sacc[v], p.c2, -lse4[j] * kLog2e));
-              pv[j] = ok ? pr : 0.f;
-              dv[j] = p.c * pv[j] * (dpacc[v] - dl4[j]);
+              pv[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[v], p.c2, -lse4[j] * kLog2e));
+              dv[j] = pv[j] * (dpacc[v] - dl4[j]);
             }
             pk[2 * g2] = pack_bf16(pv[0], pv[1]);
             pk[2 * g2 + 1] = pack_bf16(pv[2], pv[3]);
@@ -305,6 +317,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
   }
 
   if (kvalid) {
+    const float sk = p.qa * p.c;  // dK = a c acc_D
     uint16_t* krow = seq_base<uint16_t>(P.dk, p, b, e.k0, kvh) + (int64_t)key * P.dk.ss;
     uint16_t* vrow = seq_base<uint16_t>(P.dv, p, b, e.k0, kvh) + (int64_t)key * P.dv.ss;
 #pragma unroll
@@ -313,8 +326,8 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       for (int g = 0; g < 4; ++g) {
         const int c0 = d * 32 + 8 * g + 4 * hl;
         u32x2 kv, vv;
-        kv[0] = pack_bf16(p.qa * dkacc[d][4 * g], p.qa * dkacc[d][4 * g + 1]);
-        kv[1] = pack_bf16(p.qa * dkacc[d][4 * g + 2], p.qa * dkacc[d][4 * g + 3]);
+        kv[0] = pack_bf16(sk * dkacc[d][4 * g], sk * dkacc[d][4 * g + 1]);
+        kv[1] = pack_bf16(sk * dkacc[d][4 * g + 2], sk * dkacc[d][4 * g + 3]);
         vv[0] = pack_bf16(dvacc[d][4 * g], dvacc[d][4 * g + 1]);
         vv[1] = pack_bf16(dvacc[d][4 * g + 2], dvacc[d][4 * g + 3]);
         *(u32x2*)(krow + c0) = kv;

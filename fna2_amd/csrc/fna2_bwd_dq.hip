@@ -6,13 +6,15 @@
 //
 // One workgroup = 4 waves = 128 queries of one (sequence, head); wave w owns
 // queries 32w..32w+31 with Qa = [a Q | bf16(b Rq)] and dO rows in registers.
-// Per 64-key step (keys stream in by DMA through a two-stage ring):
-//   S^T, dP^T  (64 keys x 32 queries)   A operands: K | Rk and V rows (LDS)
-//   dA^T = c P^T (dP^T - delta)
-//   dQa^T += Ka^T dA^T = [dQ / a | dRq / b]^T   A operand: (K | Rk)^T by
-//                                             transpose reads
-// d_gs = (1/c) sum_i <Rq_i, (dA Rk)_i> is reduced per workgroup into a
-// partial; a fixed-order pass sums the partials (deterministic).
+// The prologue also forms delta = sum_d O dO for these queries (fp32) and
+// stores it for the dK/dV kernel, which runs after this one.
+// Per key step (keys stream in by DMA through a two-stage ring):
+//   S^T, dP^T  (keys x 32 queries)      A operands: K | Rk and V rows (LDS)
+//   dS^T = P^T (dP^T - delta)
+//   acc^T += Ka^T dS^T                  A operand: (K | Rk)^T by transpose reads
+// and the epilogue writes dQ = a c acc_D, dRq = b c acc_R.
+// d_gs = sum_i <Rq_i, (dS Rk)_i> is reduced per workgroup into a partial; a
+// fixed-order pass sums the partials (deterministic).
 #include "fna2_kernels.h"
 #include "fna2_tile.h"
 
@@ -87,6 +89,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   // Stationary B operands: Qa and dO rows of this lane's query.
   bf16x8 qreg[C::KSD + C::KSR];
   bf16x8 oreg[C::KSD];
+  u32x2 rq_epi[C::NRB > 0 ? C::NRB : 1][4];
   float lse2 = 0.f, dl = 0.f;
   {
     const uint32_t rb = (uint32_t)P.q.ss * 2u, orb = (uint32_t)P.dout.ss * 2u;
@@ -115,9 +118,40 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
         qreg[C::KSD + s] = as_bf16x8(scale_bf16x8(v, bh));
       }
     }
+    // delta = sum_d O dO for this lane's query: the lane pair (hl = 0, 1)
+    // holds the row's dO chunks, so O is read in the same layout.
+    {
+      const uint32_t yrb = (uint32_t)P.o.ss * 2u;
+      const uint16_t* yb = seq_base<const uint16_t>(P.o, p, b, e.q0, h);
+      const auto ry = make_rsrc(yb + (int64_t)q0 * P.o.ss, (uint32_t)qrows * yrb);
+      const uint32_t vy = (uint32_t)(wv * 32 + l32) * yrb + 16u * hl;
+#pragma unroll
+      for (int s = 0; s < C::KSD; ++s) {
+        const u32x4 y = __builtin_amdgcn_raw_buffer_load_b128(ry, vy + 32u * s, 0, 0);
+        const u32x4 o = as_u32x4(oreg[s]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          dl += bf16_lo(y[i]) * bf16_lo(o[i]) + bf16_hi(y[i]) * bf16_hi(o[i]);
+      }
+      dl += __shfl_xor(dl, 32);
+    }
+    if constexpr (C::NRB > 0) {
+      // raw Rq in the accumulator layout, for d_gs in the epilogue
+      const uint32_t rrb = (uint32_t)P.rq.ss * 2u;
+      const auto rr = make_rsrc(rqb + (int64_t)q0 * P.rq.ss, graph ? (uint32_t)qrows * rrb : 0u);
+      const uint32_t vr = (uint32_t)(wv * 32 + l32) * rrb + 8u * hl;
+#pragma unroll
+      for (int f = 0; f < C::NRB; ++f)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int rf = f * 32 + 8 * g + 4 * hl;
+          rq_epi[f][g] = __builtin_amdgcn_raw_buffer_load_b64(
+              rr, rf < p.R ? vr + (uint32_t)(2 * (f * 32 + 8 * g)) : kOOB, 0, 0);
+        }
+    }
     if (qvalid) {
       lse2 = seq_base<const float>(P.lse, p, b, e.q0, h)[(int64_t)qrow * P.lse.ss] * kLog2e;
-      dl = seq_base<const float>(P.delta, p, b, e.q0, h)[(int64_t)qrow * P.delta.ss];
+      if (hl == 0) seq_base<float>(P.delta, p, b, e.q0, h)[(int64_t)qrow * P.delta.ss] = dl;
     }
   }
 
@@ -155,6 +189,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
     const int kbase = it * C::BN;
     const bool active = (wq0 <= wq_last) && (!p.causal || kbase <= wq_last);
     if (!active) return;
+    const bool diag = p.causal && kbase + C::BN - 1 > wq0;
     const uint8_t* kt = cur;
     const uint8_t* rt = cur + C::KB;
     const uint8_t* vt = cur + C::KB + C::RB;
@@ -172,6 +207,16 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
       }
 #pragma unroll
       for (int s = 0; s < C::KSD; ++s) dpacc = mfma32(row_read<C::CD>(vt, row, 2 * s + hl), oreg[s], dpacc);
+      // dS^T = P^T (dP^T - delta).  Zero-filled key rows (past the
+      // sequence) and query rows give K = Rk = 0 or dO = 0 and contribute
+      // nothing, so only the causal diagonal needs a mask.
+      if (diag) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = kbase + kb2 * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
+          sacc[v] = key <= qrow ? sacc[v] : kNegInf;
+        }
+      }
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         u32x4 dk4;
@@ -181,10 +226,8 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
             const int v = 8 * half + 2 * i + j;
-            const int key = kbase + kb2 * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
-            const bool ok = qvalid && key < e.lk && (!p.causal || key <= qrow);
             const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[v], p.c2, -lse2));
-            dv2[j] = ok ? p.c * pr * (dpacc[v] - dl) : 0.f;
+            dv2[j] = pr * (dpacc[v] - dl);
           }
           dk4[i] = pack_bf16(dv2[0], dv2[1]);
         }
@@ -217,22 +260,24 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
     if (it + 1 < nkb) step(it + 1, st1, st0);
   }
 
+  // The loop accumulated dS = P (dP - delta); dA = c dS.
   float gpart = 0.f;
   if (qvalid) {
+    const float sq = p.qa * p.c;
     uint16_t* drow = seq_base<uint16_t>(P.dq, p, b, e.q0, h) + (int64_t)qrow * P.dq.ss;
 #pragma unroll
     for (int d = 0; d < C::NDB; ++d)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         u32x2 val;
-        val[0] = pack_bf16(p.qa * acc[d][4 * g], p.qa * acc[d][4 * g + 1]);
-        val[1] = pack_bf16(p.qa * acc[d][4 * g + 2], p.qa * acc[d][4 * g + 3]);
+        val[0] = pack_bf16(sq * acc[d][4 * g], sq * acc[d][4 * g + 1]);
+        val[1] = pack_bf16(sq * acc[d][4 * g + 2], sq * acc[d][4 * g + 3]);
         *(u32x2*)(drow + d * 32 + 8 * g + 4 * hl) = val;
       }
     if constexpr (C::NRB > 0) {
       if (graph) {
+        const float sr = bh * p.c;
         uint16_t* rrow = seq_base<uint16_t>(P.drq, p, b, e.q0, h) + (int64_t)qrow * P.drq.ss;
-        const uint16_t* rq = rqb + (int64_t)qrow * P.rq.ss;
 #pragma unroll
         for (int f = 0; f < C::NRB; ++f)
 #pragma unroll
@@ -240,12 +285,12 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
             const int rf = f * 32 + 8 * g + 4 * hl;
             if (rf < p.R) {
               const f32x16& a = acc[C::NDB + f];
-              const u32x2 rv = *(const u32x2*)(rq + rf);
+              const u32x2 rv = rq_epi[f][g];
               gpart += bf16_lo(rv[0]) * a[4 * g] + bf16_hi(rv[0]) * a[4 * g + 1] +
                        bf16_lo(rv[1]) * a[4 * g + 2] + bf16_hi(rv[1]) * a[4 * g + 3];
               u32x2 val;
-              val[0] = pack_bf16(bh * a[4 * g], bh * a[4 * g + 1]);
-              val[1] = pack_bf16(bh * a[4 * g + 2], bh * a[4 * g + 3]);
+              val[0] = pack_bf16(sr * a[4 * g], sr * a[4 * g + 1]);
+              val[1] = pack_bf16(sr * a[4 * g + 2], sr * a[4 * g + 3]);
               *(u32x2*)(rrow + rf) = val;
             }
           }
@@ -256,7 +301,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   for (int off = 32; off > 0; off >>= 1) gpart += __shfl_xor(gpart, off);
   if (lane == 0) red[wv] = gpart;
   __syncthreads();
-  if (tid == 0) P.dgs_partial[blockIdx.x] = ((red[0] + red[1]) + (red[2] + red[3])) / p.c;
+  if (tid == 0) P.dgs_partial[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
 // WAVES: waves per SIMD the register budget is cut for (d128/r64 needs more

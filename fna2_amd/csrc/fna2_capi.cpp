@@ -101,8 +101,6 @@ Grids grids(const fna2_problem& p) {
 int check_grids(const fna2_problem& p) {
   const Grids g = grids(p);
   if (g.fwd_grid > kMaxGrid || g.dq_grid > kMaxGrid || g.kv_grid > kMaxGrid) return FNA2_E_SHAPE;
-  const int64_t dthreads = rows_q(p) * p.heads * (p.head_dim / 8);
-  if (cdiv64(dthreads, 256) > kMaxGrid) return FNA2_E_SHAPE;
   if (rows_q(p) > INT32_MAX || rows_k(p) > INT32_MAX) return FNA2_E_SHAPE;
   return FNA2_OK;
 }
@@ -123,7 +121,7 @@ FwdWs fwd_ws(const fna2_problem& p) {
 }
 
 struct BwdWs {
-  size_t tiles_q = 0, count_q = 0, tiles_k = 0, count_k = 0, partial = 0, rqs = 0, bytes = 0;
+  size_t tiles_q = 0, count_q = 0, tiles_k = 0, count_k = 0, partial = 0, bytes = 0;
 };
 BwdWs bwd_ws(const fna2_problem& p) {
   BwdWs w;
@@ -141,10 +139,6 @@ BwdWs bwd_ws(const fna2_problem& p) {
   }
   w.partial = off;
   off += align_up(sizeof(float) * (size_t)(g.dq_grid > 0 ? g.dq_grid : 1));
-  // bf16(graph_scale / c * Rq), [rows_q][H_G][rank width]
-  w.rqs = off;
-  const int rpl = fna2::padded_rank32(p.heads_graph, p.rank);
-  off += align_up((size_t)rows_q(p) * (size_t)p.heads_graph * (size_t)rpl * 2u);
   w.bytes = off;
   return w;
 }
@@ -364,15 +358,9 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
   const Grids g = grids(p);
   K.dgs_partial = (float*)((char*)a->workspace + w.partial);
   const int rpl = fna2::padded_rank32(K.p.H_G, K.p.R);
-  K.rqs.ptr = (char*)a->workspace + w.rqs;
-  K.rqs.sh = rpl;
-  K.rqs.ss = (int64_t)p.heads_graph * rpl;
-  K.rqs.sb = p.varlen ? 0 : (int64_t)p.seqlen_q * K.rqs.ss;
 
   if (p.batch > 0 && (rows_q(p) > 0 || rows_k(p) > 0)) {
-    if (!mark(a->events, 0, stream)) return FNA2_E_LAUNCH;
-    if (fna2::launch_bwd_prep(K, rpl, stream) != hipSuccess) return FNA2_E_LAUNCH;
-    if (!mark(a->events, 1, stream)) return FNA2_E_LAUNCH;
+    if (fna2::launch_bwd_zero_uncovered(K, stream) != hipSuccess) return FNA2_E_LAUNCH;
     if (p.varlen) {
       int2* tq = (int2*)((char*)a->workspace + w.tiles_q);
       int* cq = (int*)((char*)a->workspace + w.count_q);
@@ -391,13 +379,14 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
       K.tiles_k = tk;
       K.n_tiles_k = ck;
     }
-    if (!mark(a->events, 2, stream)) return FNA2_E_LAUNCH;
-    if (rows_k(p) > 0 && fna2::launch_bwd_dkdv(K, rpl, (int)g.kv_grid, stream) != hipSuccess)
-      return FNA2_E_LAUNCH;
-    if (!mark(a->events, 3, stream) || !mark(a->events, 4, stream)) return FNA2_E_LAUNCH;
+    // dQ first: it also stores delta, which the dK/dV kernel reads.
+    if (!mark(a->events, 0, stream)) return FNA2_E_LAUNCH;
     if (rows_q(p) > 0 && fna2::launch_bwd_dq(K, rpl, (int)g.dq_grid, stream) != hipSuccess)
       return FNA2_E_LAUNCH;
-    if (!mark(a->events, 5, stream)) return FNA2_E_LAUNCH;
+    if (!mark(a->events, 1, stream) || !mark(a->events, 2, stream)) return FNA2_E_LAUNCH;
+    if (rows_k(p) > 0 && fna2::launch_bwd_dkdv(K, rpl, (int)g.kv_grid, stream) != hipSuccess)
+      return FNA2_E_LAUNCH;
+    if (!mark(a->events, 3, stream)) return FNA2_E_LAUNCH;
   }
   if (fna2::launch_bwd_dgs(K, (int)g.dq_grid, stream) != hipSuccess) return FNA2_E_LAUNCH;
   return FNA2_OK;

@@ -108,6 +108,10 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {
   return __builtin_bit_cast(bf16x8, v);
 }
 
+__device__ __forceinline__ u32x4 as_u32x4(bf16x8 v) {
+  return __builtin_bit_cast(u32x4, v);
+}
+
 __device__ __forceinline__ u32x4 ld16(const void* p) {
   return *(const u32x4*)p;
 }

@@ -16,7 +16,6 @@ struct FwdParams {
 struct BwdParams {
   Problem p;
   TView q, k, v, rq, rk, o, lse, dout, delta, dq, dk, dv, drq, drk;
-  TView rqs;             // workspace: bf16(graph_scale / c * Rq), [rows][H_G][rank width]
   const float* gs;
   float* dgs;            // [H_G]
   float* dgs_partial;    // [dq grid] per-workgroup partial sums of d_gs
@@ -43,7 +42,7 @@ inline int padded_rank32(int H_G, int R) {
 }
 
 hipError_t launch_fwd(const FwdParams& P, int rp, int grid, hipStream_t s);
-hipError_t launch_bwd_prep(const BwdParams& P, int rpl, hipStream_t s);
+hipError_t launch_bwd_zero_uncovered(const BwdParams& P, hipStream_t s);
 hipError_t launch_bwd_dkdv(const BwdParams& P, int rpl, int grid, hipStream_t s);
 hipError_t launch_bwd_dq(const BwdParams& P, int rpl, int grid, hipStream_t s);
 hipError_t launch_bwd_dgs(const BwdParams& P, int nparts, hipStream_t s);

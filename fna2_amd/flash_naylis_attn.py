@@ -137,7 +137,7 @@ class KernelTimer:
     """
 
     FWD = ("fwd",)
-    BWD = ("delta", "dkdv", "dq")
+    BWD = ("dq", "dkdv")
 
     def __init__(self, n_fwd: int, n_bwd: int):
         n = 2 * (n_fwd * len(self.FWD) + n_bwd * len(self.BWD))

@@ -105,7 +105,7 @@ typedef struct fna2_fwd_args {
 } fna2_fwd_args;
 
 #define FNA2_FWD_EVENTS 2 /* attention kernel start, end */
-#define FNA2_BWD_EVENTS 6 /* delta start/end, dK-dV start/end, dQ start/end */
+#define FNA2_BWD_EVENTS 4 /* dQ start/end, dK-dV start/end */
 
 typedef struct fna2_bwd_args {
   fna2_problem p;
@@ -114,7 +114,7 @@ typedef struct fna2_bwd_args {
   fna2_tensor out;   /* forward output                 */
   fna2_tensor lse;   /* forward LSE (fp32)             */
   fna2_tensor dout;  /* upstream gradient, like out    */
-  fna2_tensor delta; /* fp32 scratch like lse, written */
+  fna2_tensor delta; /* fp32 like lse: sum_d O dO, written */
   fna2_tensor dq;    /* like q,   written              */
   fna2_tensor dk;    /* like k,   written              */
   fna2_tensor dv;    /* like v,   written              */
@@ -124,7 +124,8 @@ typedef struct fna2_bwd_args {
   void* workspace;
   size_t workspace_bytes;
   /* Optional (may be NULL): FNA2_BWD_EVENTS hipEvent_t handles owned by the
-   * caller, recorded around the delta, dK/dV/dRk and dQ/dRq kernels. */
+   * caller, recorded around the dQ/dRq kernel (which also forms delta)
+   * and the dK/dV/dRk kernel. */
   void* const* events;
 } fna2_bwd_args;
 
