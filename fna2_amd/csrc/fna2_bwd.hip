@@ -5,7 +5,7 @@
 // FNA2/flash_naylis_attn.py:356-382, :900-921) and dK/dV/dRk are in
 // fna2_bwd_dq.hip and fna2_bwd_dkdv.hip.
 //   zero rows: varlen tokens outside [cu[0], cu[N]) get zero gradients;
-//   d_gs:      fixed-order sum of the dQ kernel's per-workgroup partials.
+//   d_gs:      fixed-order sum of the dK/dV kernel's per-wave partials.
 // Together: no atomics anywhere, bitwise deterministic, no pre-zeroing.
 //
 // Math, per head, with Qa = [a Q | b Rq], Ka = [K | Rk], S = c Qa Ka^T:
@@ -48,14 +48,16 @@ __global__ __launch_bounds__(256) void zero_uncovered_kernel(const BwdParams P, 
   }
 }
 
-// d_gs[h] = sum over dQ workgroups of head h (fixed-order tree).
+// d_gs[h] = sum of the dK/dV kernel's per-(key tile, wave) partials of head
+// h, in a fixed order (deterministic).  Varlen: the tile count is on the device.
 __global__ __launch_bounds__(256) void dgs_reduce_kernel(const float* __restrict__ part,
-                                                         int ntiles, int H,
-                                                         float* __restrict__ dgs) {
+                                                         int tiles, const int* __restrict__ n_tiles,
+                                                         int H_G, float* __restrict__ dgs) {
   __shared__ float red[4];
   const int h = blockIdx.x;
+  const int rows = 4 * (n_tiles ? min(*n_tiles, tiles) : tiles);
   float acc = 0.f;
-  for (int t = threadIdx.x; t < ntiles; t += 256) acc += part[(int64_t)t * H + h];
+  for (int t = threadIdx.x; t < rows; t += 256) acc += part[(int64_t)t * H_G + h];
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
@@ -74,10 +76,10 @@ hipError_t launch_bwd_zero_uncovered(const BwdParams& P, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_bwd_dgs(const BwdParams& P, int nparts, hipStream_t s) {
+hipError_t launch_bwd_dgs(const BwdParams& P, int tiles, hipStream_t s) {
   if (P.p.H_G <= 0) return hipSuccess;
-  hipLaunchKernelGGL(dgs_reduce_kernel, dim3(P.p.H_G), dim3(256), 0, s, P.dgs_partial,
-                     nparts / P.p.H, P.p.H, P.dgs);
+  hipLaunchKernelGGL(dgs_reduce_kernel, dim3(P.p.H_G), dim3(256), 0, s, P.dgs_partial, tiles,
+                     P.n_tiles_k, P.p.H_G, P.dgs);
   return hipGetLastError();
 }
 

@@ -49,13 +49,6 @@ struct KvCfg {
                                   (RPL > 0 ? Dma<BM, CR, NW>::PER_WAVE : 0) + 1;
 };
 
-// s_waitcnt immediate that waits until at most n vector-memory ops are in flight.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 template <int D, int RPL>
 __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
   using C = KvCfg<D, RPL>;
@@ -177,9 +170,43 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
         rl, (lds_void*)(st + C::QB + C::RB + C::OB + lslot), 4, loff, 0, 0, 0);
   };
 
+  // Per head: dRk, and this wave's d_gs partial
+  //   sum_k <Rk_k, acc_R[k]> = sum_{q,k} dS_qk <Rq_q, Rk_k>  (the head's d_gs).
+  // Lane half hl holds acc_R features 32f + 8g + 4hl + j and Rk features
+  // 16s + 8hl + e (kreg[KSD + s]); for g % 2 == hl both are local, otherwise
+  // the partner lane (lane ^ 32) holds the Rk values and sends them over.
+  // Rows of keys past the sequence have Rk = 0 and contribute nothing.
   auto write_drk = [&](int h) {
     if constexpr (C::NRB > 0) {
-      if (h < p.H_G && kvalid) {
+      if (h >= p.H_G) return;
+      float gp = 0.f;
+#pragma unroll
+      for (int f = 0; f < C::NRB; ++f) {
+        const u32x4 r0 = as_u32x4(kreg[C::KSD + 2 * f]), r1 = as_u32x4(kreg[C::KSD + 2 * f + 1]);
+        u32x2 sent[2], got[2];
+        sent[0][0] = hl ? r0[0] : r0[2];
+        sent[0][1] = hl ? r0[1] : r0[3];
+        sent[1][0] = hl ? r1[0] : r1[2];
+        sent[1][1] = hl ? r1[1] : r1[3];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) got[i][j] = __shfl_xor(sent[i][j], 32);
+        const f32x16& a = dkacc[C::NDB + f];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const u32x4& rr = (g >> 1) ? r1 : r0;
+          const bool own = (g & 1) == hl;
+          const uint32_t wa = own ? (hl ? rr[2] : rr[0]) : got[g >> 1][0];
+          const uint32_t wb = own ? (hl ? rr[3] : rr[1]) : got[g >> 1][1];
+          gp += bf16_lo(wa) * a[4 * g] + bf16_hi(wa) * a[4 * g + 1] + bf16_lo(wb) * a[4 * g + 2] +
+                bf16_hi(wb) * a[4 * g + 3];
+        }
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) gp += __shfl_xor(gp, off);
+      if (lane == 0) P.dgs_partial[((int64_t)tix * 4 + wv) * p.H_G + h] = gp;
+      if (kvalid) {
         const float sr = P.gs[h];  // dRk = b c acc_R with b c = graph_scale
         uint16_t* rrow = seq_base<uint16_t>(P.drk, p, b, e.k0, h) + (int64_t)key * P.drk.ss;
 #pragma unroll
@@ -203,8 +230,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
 
   // One query block: compute on `cur`; start the DMA for it + 2 into `nxt`.
   auto step = [&](int it, const uint8_t* cur, uint8_t* nxt) {
-    if (it + 1 < total) wait_vm<C::PER_STEP>(); else wait_vm<0>();
-    __syncthreads();
+    if (it + 1 < total) ring_barrier<C::PER_STEP>(); else ring_barrier<0>();
     if (it + 2 < total) issue(it + 2, nxt);
     __builtin_amdgcn_sched_barrier(0);
     const int hi = it / nqb;

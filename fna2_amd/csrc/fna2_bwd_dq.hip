@@ -1,8 +1,7 @@
-// fna2_bwd_dq.hip — dQ, dRq and the d_graph_scale partials for gfx950.
+// fna2_bwd_dq.hip — dQ, dRq (and delta) for gfx950.
 //
 // Replaces _fna2_bwd_dq_kernel / _fna2_bwd_dq_varlen_kernel
-// (FNA2/flash_naylis_attn.py:561-693, :1085-1208); d_graph_scale, which the
-// reference accumulates in its dK/dV kernel (:537-538, :553), is formed here.
+// (FNA2/flash_naylis_attn.py:561-693, :1085-1208).
 //
 // One workgroup = 4 waves = 128 queries of one (sequence, head); wave w owns
 // queries 32w..32w+31 with Qa = [a Q | bf16(b Rq)] and dO rows in registers.
@@ -13,8 +12,6 @@
 //   dS^T = P^T (dP^T - delta)
 //   acc^T += Ka^T dS^T                  A operand: (K | Rk)^T by transpose reads
 // and the epilogue writes dQ = a c acc_D, dRq = b c acc_R.
-// d_gs = sum_i <Rq_i, (dS Rk)_i> is reduced per workgroup into a partial; a
-// fixed-order pass sums the partials (deterministic).
 #include "fna2_kernels.h"
 #include "fna2_tile.h"
 
@@ -45,7 +42,6 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   using C = DqCfg<D, RPL>;
   __shared__ __attribute__((aligned(1024))) uint8_t st0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t st1[C::STAGE];
-  __shared__ float red[4];
   const Problem& p = P.p;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = uni(tid >> 6);
@@ -54,10 +50,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   const int tix = blockIdx.x / p.H;
   int b, qt;
   if (P.tiles_q) {
-    if (tix >= uni(*P.n_tiles_q)) {
-      if (tid == 0) P.dgs_partial[blockIdx.x] = 0.f;
-      return;
-    }
+    if (tix >= uni(*P.n_tiles_q)) return;
     const int2 t = P.tiles_q[tix];
     b = uni(t.x);
     qt = uni(t.y);
@@ -89,7 +82,6 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   // Stationary B operands: Qa and dO rows of this lane's query.
   bf16x8 qreg[C::KSD + C::KSR];
   bf16x8 oreg[C::KSD];
-  u32x2 rq_epi[C::NRB > 0 ? C::NRB : 1][4];
   float lse2 = 0.f, dl = 0.f;
   {
     const uint32_t rb = (uint32_t)P.q.ss * 2u, orb = (uint32_t)P.dout.ss * 2u;
@@ -135,20 +127,6 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
       }
       dl += __shfl_xor(dl, 32);
     }
-    if constexpr (C::NRB > 0) {
-      // raw Rq in the accumulator layout, for d_gs in the epilogue
-      const uint32_t rrb = (uint32_t)P.rq.ss * 2u;
-      const auto rr = make_rsrc(rqb + (int64_t)q0 * P.rq.ss, graph ? (uint32_t)qrows * rrb : 0u);
-      const uint32_t vr = (uint32_t)(wv * 32 + l32) * rrb + 8u * hl;
-#pragma unroll
-      for (int f = 0; f < C::NRB; ++f)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int rf = f * 32 + 8 * g + 4 * hl;
-          rq_epi[f][g] = __builtin_amdgcn_raw_buffer_load_b64(
-              rr, rf < p.R ? vr + (uint32_t)(2 * (f * 32 + 8 * g)) : kOOB, 0, 0);
-        }
-    }
     if (qvalid) {
       lse2 = seq_base<const float>(P.lse, p, b, e.q0, h)[(int64_t)qrow * P.lse.ss] * kLog2e;
       if (hl == 0) seq_base<float>(P.delta, p, b, e.q0, h)[(int64_t)qrow * P.delta.ss] = dl;
@@ -182,8 +160,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   const TrLane tl(lane);
 
   auto step = [&](int it, const uint8_t* cur, uint8_t* nxt) {
-    wait_all_loads();
-    __syncthreads();
+    ring_barrier<0>();
     if (it + 1 < nkb) issue(it + 1, nxt);
     __builtin_amdgcn_sched_barrier(0);
     const int kbase = it * C::BN;
@@ -261,7 +238,6 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   }
 
   // The loop accumulated dS = P (dP - delta); dA = c dS.
-  float gpart = 0.f;
   if (qvalid) {
     const float sq = p.qa * p.c;
     uint16_t* drow = seq_base<uint16_t>(P.dq, p, b, e.q0, h) + (int64_t)qrow * P.dq.ss;
@@ -285,9 +261,6 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
             const int rf = f * 32 + 8 * g + 4 * hl;
             if (rf < p.R) {
               const f32x16& a = acc[C::NDB + f];
-              const u32x2 rv = rq_epi[f][g];
-              gpart += bf16_lo(rv[0]) * a[4 * g] + bf16_hi(rv[0]) * a[4 * g + 1] +
-                       bf16_lo(rv[1]) * a[4 * g + 2] + bf16_hi(rv[1]) * a[4 * g + 3];
               u32x2 val;
               val[0] = pack_bf16(sr * a[4 * g], sr * a[4 * g + 1]);
               val[1] = pack_bf16(sr * a[4 * g + 2], sr * a[4 * g + 3]);
@@ -297,11 +270,6 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
       }
     }
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) gpart += __shfl_xor(gpart, off);
-  if (lane == 0) red[wv] = gpart;
-  __syncthreads();
-  if (tid == 0) P.dgs_partial[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
 // WAVES: waves per SIMD the register budget is cut for (d128/r64 needs more

@@ -78,6 +78,7 @@ struct Grids {
   int64_t fwd_grid = 0;
   int64_t dq_bound = 0, dq_grid = 0;
   int64_t kv_bound = 0, kv_grid = 0;
+  int64_t kv_tiles = 0;   // key tiles (varlen: bound)
 };
 
 Grids grids(const fna2_problem& p) {
@@ -90,10 +91,12 @@ Grids grids(const fna2_problem& p) {
     g.dq_grid = g.dq_bound * p.heads;
     g.kv_bound = fna2::tile_bound(p.total_k, p.batch, kKvBN);
     g.kv_grid = g.kv_bound * p.heads_kv;
+    g.kv_tiles = g.kv_bound;
   } else {
     g.fwd_grid = (int64_t)p.batch * cdiv64(p.seqlen_q, kFwdBM) * p.heads;
     g.dq_grid = (int64_t)p.batch * cdiv64(p.seqlen_q, kDqBM) * p.heads;
     g.kv_grid = (int64_t)p.batch * cdiv64(p.seqlen_k, kKvBN) * p.heads_kv;
+    g.kv_tiles = (int64_t)p.batch * cdiv64(p.seqlen_k, kKvBN);
   }
   return g;
 }
@@ -138,7 +141,9 @@ BwdWs bwd_ws(const fna2_problem& p) {
     off += kAlign;
   }
   w.partial = off;
-  off += align_up(sizeof(float) * (size_t)(g.dq_grid > 0 ? g.dq_grid : 1));
+  // d_gs partials: [key tiles][4 waves][H_G]
+  off += align_up(sizeof(float) * 4u * (size_t)(g.kv_tiles > 0 ? g.kv_tiles : 1) *
+                  (size_t)(p.heads_graph > 0 ? p.heads_graph : 1));
   w.bytes = off;
   return w;
 }
@@ -388,7 +393,7 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
       return FNA2_E_LAUNCH;
     if (!mark(a->events, 3, stream)) return FNA2_E_LAUNCH;
   }
-  if (fna2::launch_bwd_dgs(K, (int)g.dq_grid, stream) != hipSuccess) return FNA2_E_LAUNCH;
+  if (fna2::launch_bwd_dgs(K, (int)g.kv_tiles, stream) != hipSuccess) return FNA2_E_LAUNCH;
   return FNA2_OK;
 }
 

@@ -142,8 +142,7 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
   // One key tile: wait for its DMA, start the next one into the other stage,
   // then compute on this one.
   auto step = [&](int kt, const uint8_t* cur, uint8_t* nxt) {
-    wait_all_loads();
-    __syncthreads();
+    ring_barrier<0>();
     if (kt + 1 < nkv) issue(kt + 1, nxt);
     __builtin_amdgcn_sched_barrier(0);  // keep the whole prefetch ahead of the compute
     const int kbase = kt * C::BN;

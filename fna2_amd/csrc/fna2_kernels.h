@@ -18,7 +18,7 @@ struct BwdParams {
   TView q, k, v, rq, rk, o, lse, dout, delta, dq, dk, dv, drq, drk;
   const float* gs;
   float* dgs;            // [H_G]
-  float* dgs_partial;    // [dq grid] per-workgroup partial sums of d_gs
+  float* dgs_partial;    // [key tiles][4 waves][H_G] partial sums of d_gs
   const int2* tiles_q;   // varlen: query tiles (dQ kernel)
   const int* n_tiles_q;
   const int2* tiles_k;   // varlen: key tiles (dK/dV kernel)
@@ -45,6 +45,6 @@ hipError_t launch_fwd(const FwdParams& P, int rp, int grid, hipStream_t s);
 hipError_t launch_bwd_zero_uncovered(const BwdParams& P, hipStream_t s);
 hipError_t launch_bwd_dkdv(const BwdParams& P, int rpl, int grid, hipStream_t s);
 hipError_t launch_bwd_dq(const BwdParams& P, int rpl, int grid, hipStream_t s);
-hipError_t launch_bwd_dgs(const BwdParams& P, int nparts, hipStream_t s);
+hipError_t launch_bwd_dgs(const BwdParams& P, int kv_tiles, hipStream_t s);
 
 }  // namespace fna2

@@ -78,6 +78,25 @@ struct Dma {
     }
   }
 
+  // Issue without a plan: the lane offsets are formed on the fly (for tiles
+  // that are loaded rarely, where holding the offsets would cost registers).
+  __device__ __forceinline__ static void issue_direct(__amdgpu_buffer_rsrc_t rs, uint8_t* lds,
+                                                      int wave, int lane, uint32_t row_bytes,
+                                                      int valid_chunks) {
+#pragma unroll
+    for (int j = 0; j < PER_WAVE; ++j) {
+      const int i = wave + j * NWAVE;
+      const int p = 64 * i + lane;
+      const int row = p / C;
+      const int col = (p % C) ^ swz<C>(row);
+      const uint32_t off = col < valid_chunks ? (uint32_t)row * row_bytes + (uint32_t)col * 16u
+                                              : kOOB;
+      if (i < N)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(lds + i * 1024), 16, off, 0, 0,
+                                                 0);
+    }
+  }
+
   // Issue this wave's share of the tile into LDS at `lds` (tile base).
   __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, uint8_t* lds, int wave) const {
 #pragma unroll
@@ -124,6 +143,20 @@ __device__ __forceinline__ bf16x8 tr_operand(const uint8_t* tile, const TrLane& 
   return __builtin_bit_cast(bf16x8, ab);
 }
 
-__device__ __forceinline__ void wait_all_loads() { __builtin_amdgcn_s_waitcnt(0); }
+// Ring barrier: wait until at most N of this wave's vector-memory operations
+// (tile DMA included) are in flight and its LDS reads are done, then barrier
+// the workgroup.  Each wave waits for its own DMA before the barrier, so after
+// it every wave's part of the older tiles is in LDS.  __syncthreads() is not
+// used because its release fence waits for every in-flight LDS DMA (vmcnt(0))
+// and so would drain the prefetch ring at each step.  The signal fences stop
+// the compiler from moving memory accesses across the barrier.
+template <int N>
+__device__ __forceinline__ void ring_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 
 }  // namespace fna2

@@ -171,8 +171,8 @@ def test_bwd_workspace_is_small_and_rank_free(lib):
                 cu_seqlens_q=None, cu_seqlens_k=None)
     w32 = lib.fna2_bwd_workspace_bytes(ctypes.byref(_capi.Problem(rank=32, **base)))
     w64 = lib.fna2_bwd_workspace_bytes(ctypes.byref(_capi.Problem(rank=64, **base)))
-    # dense: one fp32 d_graph_scale partial per dQ workgroup (2 x 2 tiles x 8 heads), 256-aligned
-    assert w32 == w64 == 256
+    # dense: fp32 d_graph_scale partials per (key tile, wave, graph head): 2 x 2 x 4 x 8
+    assert w32 == w64 == 2 * 2 * 4 * 8 * 4
 
 
 def test_python_errors_map_to_assertion(lib):
