@@ -5,7 +5,7 @@
 // FNA2/flash_naylis_attn.py:356-382, :900-921) and dK/dV/dRk are in
 // fna2_bwd_dq.hip and fna2_bwd_dkdv.hip.
 //   zero rows: varlen tokens outside [cu[0], cu[N]) get zero gradients;
-//   d_gs:      fixed-order sum of the dK/dV kernel's per-wave partials.
+//   d_gs:      fixed-order sum of the dQ kernel's per-wave partials.
 // Together: no atomics anywhere, bitwise deterministic, no pre-zeroing.
 //
 // Math, per head, with Qa = [a Q | b Rq], Ka = [K | Rk], S = c Qa Ka^T:
@@ -48,8 +48,8 @@ __global__ __launch_bounds__(256) void zero_uncovered_kernel(const BwdParams P, 
   }
 }
 
-// d_gs[h] = sum of the dK/dV kernel's per-(key tile, wave) partials of head
-// h, in a fixed order (deterministic).  Varlen: the tile count is on the device.
+// d_gs[h] = sum of the dQ kernel's per-(query tile, wave) partials of head h,
+// in a fixed order (deterministic).  Varlen: the tile count is on the device.
 __global__ __launch_bounds__(256) void dgs_reduce_kernel(const float* __restrict__ part,
                                                          int tiles, const int* __restrict__ n_tiles,
                                                          int H_G, float* __restrict__ dgs) {
@@ -79,7 +79,7 @@ hipError_t launch_bwd_zero_uncovered(const BwdParams& P, hipStream_t s) {
 hipError_t launch_bwd_dgs(const BwdParams& P, int tiles, hipStream_t s) {
   if (P.p.H_G <= 0) return hipSuccess;
   hipLaunchKernelGGL(dgs_reduce_kernel, dim3(P.p.H_G), dim3(256), 0, s, P.dgs_partial, tiles,
-                     P.n_tiles_k, P.p.H_G, P.dgs);
+                     P.n_tiles_q, P.p.H_G, P.dgs);
   return hipGetLastError();
 }
 

@@ -6,12 +6,14 @@
 // One workgroup = 4 waves = 128 queries of one (sequence, head); wave w owns
 // queries 32w..32w+31 with Qa = [a Q | bf16(b Rq)] and dO rows in registers.
 // The prologue also forms delta = sum_d O dO for these queries (fp32) and
-// stores it for the dK/dV kernel, which runs after this one.
+// stores it, -LSE log2(e) and the rounded bias operand bf16(b Rq) for the
+// dK/dV kernel, which runs after this one.
 // Per key step (keys stream in by DMA through a two-stage ring):
 //   S^T, dP^T  (keys x 32 queries)      A operands: K | Rk and V rows (LDS)
 //   dS^T = P^T (dP^T - delta)
 //   acc^T += Ka^T dS^T                  A operand: (K | Rk)^T by transpose reads
-// and the epilogue writes dQ = a c acc_D, dRq = b c acc_R.
+// and the epilogue writes dQ = a c acc_D, dRq = b c acc_R and the wave's
+// partial of d_gs = sum_i <Rq_i, (dS Rk)_i> (a fixed-order pass sums them).
 #include "fna2_kernels.h"
 #include "fna2_tile.h"
 
@@ -49,17 +51,16 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   const int h = blockIdx.x % p.H;
   const int tix = blockIdx.x / p.H;
   int b, qt;
+  SeqExt e;
   if (P.tiles_q) {
     if (tix >= uni(*P.n_tiles_q)) return;
-    const int2 t = P.tiles_q[tix];
-    b = uni(t.x);
-    qt = uni(t.y);
+    tile_decode(P.tiles_q, tix, b, qt, e);
   } else {
     const int nqt = cdiv(p.sq, C::BM);
     b = tix % p.nseq;
     qt = nqt - 1 - tix / p.nseq;
+    e = seq_ext_uniform(p, b);
   }
-  const SeqExt e = seq_ext_uniform(p, b);
   const int kvh = h / p.group;
   const bool graph = (RPL > 0) && (h < p.H_G);
   const float bh = graph ? P.gs[h] / p.c : 0.f;
@@ -82,6 +83,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   // Stationary B operands: Qa and dO rows of this lane's query.
   bf16x8 qreg[C::KSD + C::KSR];
   bf16x8 oreg[C::KSD];
+  u32x2 rq_epi[C::NRB > 0 ? C::NRB : 1][4];  // raw Rq, accumulator layout (d_gs)
   float lse2 = 0.f, dl = 0.f;
   {
     const uint32_t rb = (uint32_t)P.q.ss * 2u, orb = (uint32_t)P.dout.ss * 2u;
@@ -109,6 +111,20 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
         u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rr, in ? vr + 32u * s : kOOB, 0, 0);
         qreg[C::KSD + s] = as_bf16x8(scale_bf16x8(v, bh));
       }
+      // The dK/dV kernel streams the same rounded operand bf16(b Rq).
+      if (graph && qvalid) {
+        uint16_t* srow = seq_base<uint16_t>(P.rqs, p, b, e.q0, h) + (int64_t)qrow * P.rqs.ss;
+#pragma unroll
+        for (int s = 0; s < C::KSR; ++s) st16(srow + 16 * s + 8 * hl, as_u32x4(qreg[C::KSD + s]));
+      }
+#pragma unroll
+      for (int f = 0; f < C::NRB; ++f)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int rf = f * 32 + 8 * g + 4 * hl;
+          rq_epi[f][g] = __builtin_amdgcn_raw_buffer_load_b64(
+              rr, rf < p.R ? (uint32_t)(wv * 32 + l32) * rrb + 2u * rf : kOOB, 0, 0);
+        }
     }
     // delta = sum_d O dO for this lane's query: the lane pair (hl = 0, 1)
     // holds the row's dO chunks, so O is read in the same layout.
@@ -129,7 +145,10 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
     }
     if (qvalid) {
       lse2 = seq_base<const float>(P.lse, p, b, e.q0, h)[(int64_t)qrow * P.lse.ss] * kLog2e;
-      if (hl == 0) seq_base<float>(P.delta, p, b, e.q0, h)[(int64_t)qrow * P.delta.ss] = dl;
+      if (hl == 0) {
+        seq_base<float>(P.delta, p, b, e.q0, h)[(int64_t)qrow * P.delta.ss] = dl;
+        seq_base<float>(P.nlse, p, b, e.q0, h)[(int64_t)qrow * P.nlse.ss] = -lse2;
+      }
     }
   }
 
@@ -158,6 +177,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
 #pragma unroll
   for (int i = 0; i < C::NDB + C::NRB; ++i) acc[i] = f32x16{};
   const TrLane tl(lane);
+  const RowLane rdl(lane);
 
   auto step = [&](int it, const uint8_t* cur, uint8_t* nxt) {
     ring_barrier<0>();
@@ -173,17 +193,16 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
     bf16x8 db[C::NKB][2];
 #pragma unroll
     for (int kb2 = 0; kb2 < C::NKB; ++kb2) {
-      const int row = kb2 * 32 + l32;
       f32x16 sacc = f32x16{}, dpacc = f32x16{};
 #pragma unroll
-      for (int s = 0; s < C::KSD; ++s) sacc = mfma32(row_read<C::CD>(kt, row, 2 * s + hl), qreg[s], sacc);
+      for (int s = 0; s < C::KSD; ++s) sacc = mfma32(row_read<C::BN>(kt, rdl, kb2 * 32, s), qreg[s], sacc);
       if constexpr (C::KSR > 0) {
 #pragma unroll
         for (int s = 0; s < C::KSR; ++s)
-          if (s < nrs) sacc = mfma32(row_read<C::CR>(rt, row, 2 * s + hl), qreg[C::KSD + s], sacc);
+          if (s < nrs) sacc = mfma32(row_read<C::BN>(rt, rdl, kb2 * 32, s), qreg[C::KSD + s], sacc);
       }
 #pragma unroll
-      for (int s = 0; s < C::KSD; ++s) dpacc = mfma32(row_read<C::CD>(vt, row, 2 * s + hl), oreg[s], dpacc);
+      for (int s = 0; s < C::KSD; ++s) dpacc = mfma32(row_read<C::BN>(vt, rdl, kb2 * 32, s), oreg[s], dpacc);
       // dS^T = P^T (dP^T - delta).  Zero-filled key rows (past the
       // sequence) and query rows give K = Rk = 0 or dO = 0 and contribute
       // nothing, so only the causal diagonal needs a mask.
@@ -219,13 +238,13 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
         const int k0 = kb2 * 32 + 16 * half;
 #pragma unroll
         for (int f = 0; f < C::NDB; ++f)
-          acc[f] = mfma32(tr_operand<C::CD>(kt, tl, k0, 32 * f), db[kb2][half], acc[f]);
+          acc[f] = mfma32(tr_operand<C::BN>(kt, tl, k0, 32 * f), db[kb2][half], acc[f]);
         if constexpr (C::NRB > 0) {
           if (graph) {
 #pragma unroll
             for (int f = 0; f < C::NRB; ++f)
               acc[C::NDB + f] =
-                  mfma32(tr_operand<C::CR>(rt, tl, k0, 32 * f), db[kb2][half], acc[C::NDB + f]);
+                  mfma32(tr_operand<C::BN>(rt, tl, k0, 32 * f), db[kb2][half], acc[C::NDB + f]);
           }
         }
       }
@@ -238,6 +257,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   }
 
   // The loop accumulated dS = P (dP - delta); dA = c dS.
+  float gpart = 0.f;
   if (qvalid) {
     const float sq = p.qa * p.c;
     uint16_t* drow = seq_base<uint16_t>(P.dq, p, b, e.q0, h) + (int64_t)qrow * P.dq.ss;
@@ -261,6 +281,9 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
             const int rf = f * 32 + 8 * g + 4 * hl;
             if (rf < p.R) {
               const f32x16& a = acc[C::NDB + f];
+              const u32x2 rv = rq_epi[f][g];
+              gpart += bf16_lo(rv[0]) * a[4 * g] + bf16_hi(rv[0]) * a[4 * g + 1] +
+                       bf16_lo(rv[1]) * a[4 * g + 2] + bf16_hi(rv[1]) * a[4 * g + 3];
               u32x2 val;
               val[0] = pack_bf16(sr * a[4 * g], sr * a[4 * g + 1]);
               val[1] = pack_bf16(sr * a[4 * g + 2], sr * a[4 * g + 3]);
@@ -268,6 +291,14 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
             }
           }
       }
+    }
+  }
+  // d_gs partial of this wave: sum_i <Rq_i, (dS Rk)_i> over its queries.
+  if constexpr (C::NRB > 0) {
+    if (graph) {
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) gpart += __shfl_xor(gpart, off);
+      if (lane == 0) P.dgs_partial[((int64_t)tix * 4 + wv) * p.H_G + h] = gpart;
     }
   }
 }

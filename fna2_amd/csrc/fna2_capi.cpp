@@ -79,6 +79,7 @@ struct Grids {
   int64_t dq_bound = 0, dq_grid = 0;
   int64_t kv_bound = 0, kv_grid = 0;
   int64_t kv_tiles = 0;   // key tiles (varlen: bound)
+  int64_t q_tiles = 0;    // dQ query tiles (varlen: bound)
 };
 
 Grids grids(const fna2_problem& p) {
@@ -92,11 +93,13 @@ Grids grids(const fna2_problem& p) {
     g.kv_bound = fna2::tile_bound(p.total_k, p.batch, kKvBN);
     g.kv_grid = g.kv_bound * p.heads_kv;
     g.kv_tiles = g.kv_bound;
+    g.q_tiles = g.dq_bound;
   } else {
     g.fwd_grid = (int64_t)p.batch * cdiv64(p.seqlen_q, kFwdBM) * p.heads;
     g.dq_grid = (int64_t)p.batch * cdiv64(p.seqlen_q, kDqBM) * p.heads;
     g.kv_grid = (int64_t)p.batch * cdiv64(p.seqlen_k, kKvBN) * p.heads_kv;
     g.kv_tiles = (int64_t)p.batch * cdiv64(p.seqlen_k, kKvBN);
+    g.q_tiles = (int64_t)p.batch * cdiv64(p.seqlen_q, kDqBM);
   }
   return g;
 }
@@ -117,14 +120,15 @@ FwdWs fwd_ws(const fna2_problem& p) {
   const Grids g = grids(p);
   if (p.varlen && g.fwd_bound > 0) {
     w.tiles = 0;
-    w.count = align_up(sizeof(int2) * g.fwd_bound);
+    w.count = align_up(sizeof(fna2::TileRec) * g.fwd_bound);
     w.bytes = w.count + kAlign;
   }
   return w;
 }
 
 struct BwdWs {
-  size_t tiles_q = 0, count_q = 0, tiles_k = 0, count_k = 0, partial = 0, bytes = 0;
+  size_t tiles_q = 0, count_q = 0, tiles_k = 0, count_k = 0, partial = 0, rqs = 0, nlse = 0;
+  size_t bytes = 0;
 };
 BwdWs bwd_ws(const fna2_problem& p) {
   BwdWs w;
@@ -132,18 +136,25 @@ BwdWs bwd_ws(const fna2_problem& p) {
   size_t off = 0;
   if (p.varlen && g.dq_bound > 0) {
     w.tiles_q = off;
-    off += align_up(sizeof(int2) * g.dq_bound);
+    off += align_up(sizeof(fna2::TileRec) * g.dq_bound);
     w.count_q = off;
     off += kAlign;
     w.tiles_k = off;
-    off += align_up(sizeof(int2) * g.kv_bound);
+    off += align_up(sizeof(fna2::TileRec) * g.kv_bound);
     w.count_k = off;
     off += kAlign;
   }
   w.partial = off;
-  // d_gs partials: [key tiles][4 waves][H_G]
-  off += align_up(sizeof(float) * 4u * (size_t)(g.kv_tiles > 0 ? g.kv_tiles : 1) *
+  // d_gs partials: [query tiles][4 waves][H_G]
+  off += align_up(sizeof(float) * 4u * (size_t)(g.q_tiles > 0 ? g.q_tiles : 1) *
                   (size_t)(p.heads_graph > 0 ? p.heads_graph : 1));
+  // bf16(graph_scale / c * Rq), [rows_q][H_G][rank width]
+  w.rqs = off;
+  const int rpl = fna2::padded_rank32(p.heads_graph, p.rank);
+  off += align_up((size_t)rows_q(p) * (size_t)p.heads_graph * (size_t)rpl * 2u);
+  // -LSE log2(e), fp32 [rows_q][H]
+  w.nlse = off;
+  off += align_up((size_t)rows_q(p) * (size_t)p.heads * 4u);
   w.bytes = off;
   return w;
 }
@@ -201,10 +212,12 @@ int max_iters(const fna2_problem& p, int hint, int total, int step) {
   return (int)std::min<int64_t>(cdiv64(n, step), 1 << 20);
 }
 
-// Kernels exist for gfx950 only; cache the answer per device.
-int check_device() {
+// Kernels exist for gfx950 only; cache the answer (and the CU count, which
+// sizes the persistent grids) per device.
+int check_device(int* num_cus = nullptr) {
   static std::mutex mu;
   static int state[64] = {0};  // 0 unknown, 1 ok, -1 wrong arch
+  static int cus[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return FNA2_E_DEVICE;
   if (dev < 0 || dev >= 64) return FNA2_E_DEVICE;
@@ -213,7 +226,9 @@ int check_device() {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return FNA2_E_DEVICE;
     state[dev] = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
+    cus[dev] = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 1;
   }
+  if (num_cus) *num_cus = cus[dev];
   return state[dev] == 1 ? FNA2_OK : FNA2_E_DEVICE;
 }
 
@@ -319,7 +334,7 @@ int fna2_fwd(const fna2_fwd_args* a, void* stream_ptr) {
   const Grids g = grids(p);
   if (p.varlen) {
     const FwdWs w = fwd_ws(p);
-    int2* tiles = (int2*)((char*)a->workspace + w.tiles);
+    fna2::TileRec* tiles = (fna2::TileRec*)((char*)a->workspace + w.tiles);
     int* count = (int*)((char*)a->workspace + w.count);
     fna2::TileSpec spec{0, kFwdBM, kFwdBN};
     if (fna2::launch_build_tiles(K.p, spec, max_iters(p, p.seqlen_k, p.total_k, kFwdBN), tiles,
@@ -338,7 +353,8 @@ int fna2_fwd(const fna2_fwd_args* a, void* stream_ptr) {
 int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
   FNA2_TRY(fna2_check_bwd(a));
   const fna2_problem& p = a->p;
-  FNA2_TRY(check_device());
+  int n_cu = 1;
+  FNA2_TRY(check_device(&n_cu));
   hipStream_t stream = (hipStream_t)stream_ptr;
   fna2::BwdParams K;
   std::memset(&K, 0, sizeof(K));
@@ -363,13 +379,21 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
   const Grids g = grids(p);
   K.dgs_partial = (float*)((char*)a->workspace + w.partial);
   const int rpl = fna2::padded_rank32(K.p.H_G, K.p.R);
+  K.rqs.ptr = (char*)a->workspace + w.rqs;
+  K.rqs.sh = rpl;
+  K.rqs.ss = (int64_t)p.heads_graph * rpl;
+  K.rqs.sb = p.varlen ? 0 : (int64_t)p.seqlen_q * K.rqs.ss;
+  K.nlse.ptr = (char*)a->workspace + w.nlse;
+  K.nlse.sh = 1;
+  K.nlse.ss = p.heads;
+  K.nlse.sb = p.varlen ? 0 : (int64_t)p.seqlen_q * p.heads;
 
   if (p.batch > 0 && (rows_q(p) > 0 || rows_k(p) > 0)) {
     if (fna2::launch_bwd_zero_uncovered(K, stream) != hipSuccess) return FNA2_E_LAUNCH;
     if (p.varlen) {
-      int2* tq = (int2*)((char*)a->workspace + w.tiles_q);
+      fna2::TileRec* tq = (fna2::TileRec*)((char*)a->workspace + w.tiles_q);
       int* cq = (int*)((char*)a->workspace + w.count_q);
-      int2* tk = (int2*)((char*)a->workspace + w.tiles_k);
+      fna2::TileRec* tk = (fna2::TileRec*)((char*)a->workspace + w.tiles_k);
       int* ck = (int*)((char*)a->workspace + w.count_k);
       fna2::TileSpec sq{0, kDqBM, kDqBN};
       fna2::TileSpec sk{1, kKvBN, kKvBM};
@@ -389,11 +413,13 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
     if (rows_q(p) > 0 && fna2::launch_bwd_dq(K, rpl, (int)g.dq_grid, stream) != hipSuccess)
       return FNA2_E_LAUNCH;
     if (!mark(a->events, 1, stream) || !mark(a->events, 2, stream)) return FNA2_E_LAUNCH;
-    if (rows_k(p) > 0 && fna2::launch_bwd_dkdv(K, rpl, (int)g.kv_grid, stream) != hipSuccess)
+    // persistent: one workgroup per CU walks the (key tile, KV head) items
+    const int kv_grid = (int)std::min<int64_t>(g.kv_grid, n_cu);
+    if (rows_k(p) > 0 && fna2::launch_bwd_dkdv(K, rpl, kv_grid, stream) != hipSuccess)
       return FNA2_E_LAUNCH;
     if (!mark(a->events, 3, stream)) return FNA2_E_LAUNCH;
   }
-  if (fna2::launch_bwd_dgs(K, (int)g.kv_tiles, stream) != hipSuccess) return FNA2_E_LAUNCH;
+  if (fna2::launch_bwd_dgs(K, (int)g.q_tiles, stream) != hipSuccess) return FNA2_E_LAUNCH;
   return FNA2_OK;
 }
 

@@ -92,6 +92,23 @@ __device__ __forceinline__ SeqExt seq_ext_uniform(const Problem& p, int b) {
   return u;
 }
 
+// A varlen work tile: sequence b, tile t within it and the sequence's clamped
+// extents, so that a kernel decodes a tile with one 32-byte scalar load.
+struct __attribute__((aligned(32))) TileRec {
+  int b, t, q0, lq, k0, lk, pad0, pad1;
+};
+
+__device__ __forceinline__ void tile_decode(const TileRec* __restrict__ tiles, int tix, int& b,
+                                            int& t, SeqExt& e) {
+  const TileRec r = tiles[tix];
+  b = uni(r.b);
+  t = uni(r.t);
+  e.q0 = uni(r.q0);
+  e.lq = uni(r.lq);
+  e.k0 = uni(r.k0);
+  e.lk = uni(r.lk);
+}
+
 // Base pointer of sequence b, head h of a view; row r is at base + r * ss.
 template <typename T>
 __device__ __forceinline__ T* seq_base(const TView& t, const Problem& p, int b,

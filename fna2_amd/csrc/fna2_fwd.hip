@@ -50,17 +50,16 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
   const int h = blockIdx.x % p.H;
   const int tix = blockIdx.x / p.H;
   int b, qt;
+  SeqExt e;
   if (P.tiles) {
     if (tix >= uni(*P.n_tiles)) return;
-    const int2 t = P.tiles[tix];
-    b = uni(t.x);
-    qt = uni(t.y);
+    tile_decode(P.tiles, tix, b, qt, e);
   } else {
     const int nqt = cdiv(p.sq, C::BM);
     b = tix % p.nseq;
     qt = nqt - 1 - tix / p.nseq;  // longest causal tiles first
+    e = seq_ext_uniform(p, b);
   }
-  const SeqExt e = seq_ext_uniform(p, b);
   const int kvh = h / p.group;
   const bool graph = (RPL > 0) && (h < p.H_G);
   const float bh = graph ? P.gs[h] / p.c : 0.f;
@@ -138,6 +137,7 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
   for (int d = 0; d < D / 32; ++d) oacc[d] = f32x16{};
   float m_i = kNegInf, l_i = 0.f;
   const TrLane tl(lane);
+  const RowLane rdl(lane);
 
   // One key tile: wait for its DMA, start the next one into the other stage,
   // then compute on this one.
@@ -156,13 +156,12 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
 #pragma unroll
     for (int kb2 = 0; kb2 < C::BN / 32; ++kb2) {
       f32x16 acc = f32x16{};
-      const int row = kb2 * 32 + l32;
 #pragma unroll
-      for (int s = 0; s < C::KSD; ++s) acc = mfma32(row_read<C::CD>(kl, row, 2 * s + hl), qreg[s], acc);
+      for (int s = 0; s < C::KSD; ++s) acc = mfma32(row_read<C::BN>(kl, rdl, kb2 * 32, s), qreg[s], acc);
       if constexpr (C::KSR > 0) {
 #pragma unroll
         for (int s = 0; s < C::KSR; ++s)
-          if (s < nrs) acc = mfma32(row_read<C::CR>(rl, row, 2 * s + hl), qreg[C::KSD + s], acc);
+          if (s < nrs) acc = mfma32(row_read<C::BN>(rl, rdl, kb2 * 32, s), qreg[C::KSD + s], acc);
       }
       sacc[kb2] = acc;
     }
@@ -212,7 +211,7 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
     for (int s = 0; s < C::BN / 16; ++s)
 #pragma unroll
       for (int d = 0; d < D / 32; ++d)
-        oacc[d] = mfma32(tr_operand<C::CD>(vl, tl, 16 * s, 32 * d), pb[s], oacc[d]);
+        oacc[d] = mfma32(tr_operand<C::BN>(vl, tl, 16 * s, 32 * d), pb[s], oacc[d]);
   };
 
   if (nkv > 0) issue(0, stage0);

@@ -9,19 +9,22 @@ struct FwdParams {
   Problem p;
   TView q, k, v, rq, rk, o, lse;
   const float* gs;
-  const int2* tiles;   // varlen: device tile list (null in dense mode)
+  const TileRec* tiles;  // varlen: device tile list (null in dense mode)
   const int* n_tiles;  // varlen: device tile count
 };
 
 struct BwdParams {
   Problem p;
   TView q, k, v, rq, rk, o, lse, dout, delta, dq, dk, dv, drq, drk;
+  // Workspace written by the dQ kernel for the dK/dV kernel:
+  TView rqs;   // bf16(b_h Rq), [rows][H_G][rank width]
+  TView nlse;  // -LSE log2(e), fp32 [rows][H]
   const float* gs;
   float* dgs;            // [H_G]
-  float* dgs_partial;    // [key tiles][4 waves][H_G] partial sums of d_gs
-  const int2* tiles_q;   // varlen: query tiles (dQ kernel)
+  float* dgs_partial;    // [query tiles][4 waves][H_G] partial sums of d_gs
+  const TileRec* tiles_q;  // varlen: query tiles (dQ kernel)
   const int* n_tiles_q;
-  const int2* tiles_k;   // varlen: key tiles (dK/dV kernel)
+  const TileRec* tiles_k;  // varlen: key tiles (dK/dV kernel)
   const int* n_tiles_k;
 };
 
@@ -45,6 +48,6 @@ hipError_t launch_fwd(const FwdParams& P, int rp, int grid, hipStream_t s);
 hipError_t launch_bwd_zero_uncovered(const BwdParams& P, hipStream_t s);
 hipError_t launch_bwd_dkdv(const BwdParams& P, int rpl, int grid, hipStream_t s);
 hipError_t launch_bwd_dq(const BwdParams& P, int rpl, int grid, hipStream_t s);
-hipError_t launch_bwd_dgs(const BwdParams& P, int kv_tiles, hipStream_t s);
+hipError_t launch_bwd_dgs(const BwdParams& P, int q_tiles, hipStream_t s);
 
 }  // namespace fna2

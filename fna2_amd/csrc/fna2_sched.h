@@ -21,10 +21,10 @@ inline int64_t tile_bound(int64_t extent, int64_t nseq, int tile) {
 
 int tile_buckets(int max_iters);
 
-// Builds `tiles` (int2 {sequence, tile}) ordered by descending work and writes
+// Builds `tiles` (TileRec: sequence, tile, extents) ordered by descending work and writes
 // the number of tiles to *count.  One workgroup.
 hipError_t launch_build_tiles(const Problem& p, const TileSpec& spec,
-                              int max_iters, int2* tiles, int* count, int cap,
+                              int max_iters, TileRec* tiles, int* count, int cap,
                               hipStream_t stream);
 
 }  // namespace fna2

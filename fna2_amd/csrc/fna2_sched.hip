@@ -33,7 +33,7 @@ __device__ __forceinline__ int tile_work(const SeqExt& e, const TileSpec& s,
 }
 
 __global__ __launch_bounds__(kThreads) void build_tiles_kernel(
-    Problem p, TileSpec spec, int nbuckets, int2* __restrict__ tiles,
+    Problem p, TileSpec spec, int nbuckets, TileRec* __restrict__ tiles,
     int* __restrict__ count, int cap) {
   __shared__ int hist[kMaxBuckets];
   __shared__ int warp_tot[kThreads / 64];
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(kThreads) void build_tiles_kernel(
     for (int t = 0; t < n; ++t) {
       int w = min(tile_work(e, spec, p.causal, t), nbuckets - 1);
       int pos = atomicAdd(&hist[nbuckets - 1 - w], 1);
-      if (pos < cap) tiles[pos] = make_int2(b, t);
+      if (pos < cap) tiles[pos] = TileRec{b, t, e.q0, e.lq, e.k0, e.lk, 0, 0};
     }
   }
 }
@@ -103,7 +103,7 @@ int tile_buckets(int max_iters) {
 }
 
 hipError_t launch_build_tiles(const Problem& p, const TileSpec& spec,
-                              int max_iters, int2* tiles, int* count, int cap,
+                              int max_iters, TileRec* tiles, int* count, int cap,
                               hipStream_t stream) {
   hipLaunchKernelGGL(build_tiles_kernel, dim3(1), dim3(kThreads), 0, stream, p,
                      spec, tile_buckets(max_iters), tiles, count, cap);

@@ -1,18 +1,26 @@
 // fna2_tile.h — LDS tile machinery for the gfx950 kernels.
 //
-// Tiles are row-major in LDS (one row = one token, C 16-byte chunks of 8
-// bf16) with the chunk index XOR-swizzled per row, so that both readers
-// below are free of bank conflicts (checked for 32- and 64-bank LDS):
+// A tile holds ROWS rows (one row = one token) of C 16-byte chunks (8 bf16
+// each), C a multiple of 4.  The row is split into column groups of 4 chunks
+// (32 features); group g is a ROWS x 64-byte sub-tile, and inside a row the
+// 4 chunks of a group are XOR-swizzled by a 2-bit function of row bits 1..3:
+//   offset(row, chunk) = (chunk / 4) * ROWS * 64 + row * 64
+//                        + ((chunk % 4) ^ swz4(row)) * 16.
+// Both readers below are free of bank conflicts with 32 and with 64 banks:
 //   * row reads: ds_read_b128 by 32 lanes on 32 consecutive rows at the same
 //     logical chunk (the natural MFMA operand, k = features);
 //   * transpose reads: ds_read_b64_tr_b16 where each 16-lane group reads 4
-//     consecutive rows x 4 consecutive chunks (an MFMA operand with k = rows).
+//     consecutive rows x 2 consecutive chunks (an MFMA operand with k = rows).
+// Because the swizzle only permutes chunks inside a group and only depends on
+// row bits 1..3, moving a read by a multiple of 16 rows or by whole column
+// groups moves its address by a constant: a lane needs two offsets for all
+// its row reads of a tile and two for all its transpose reads, and every
+// other term is an instruction immediate.
 // Tiles are filled by buffer_load ... lds (global -> LDS DMA, no VGPR
 // staging).  A wave-level DMA instruction writes 64 consecutive 16-byte
-// chunks; each lane fetches the logical chunk that belongs at its physical
-// slot.  Rows beyond the tensor's valid range and chunks beyond the feature
-// count are fetched from an out-of-range offset, which the buffer unit
-// returns as zeros.
+// slots; each lane fetches the logical chunk that belongs at its slot.  Rows
+// beyond the tensor's valid range and chunks beyond the feature count are
+// fetched from an out-of-range offset, which the buffer unit returns as zeros.
 #pragma once
 
 #include "fna2_device.h"
@@ -39,19 +47,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                            (int)kRsrcWord3);
 }
 
-// Per-row chunk swizzle for rows of C chunks (C in {4, 8, 16}); depends on r % 16.
-template <int C>
-__device__ __forceinline__ int swz(int r) {
-  const int x = r & 15;
-  if constexpr (C == 4) return (x ^ (x >> 2)) & 3;
-  else if constexpr (C == 8) return (x ^ (x >> 2) ^ ((x >> 1) << 2)) & 7;
-  else return (x ^ (x << 2)) & 15;
+// 2-bit chunk swizzle of a row (row bits 1..3).
+__device__ __forceinline__ int swz4(int r) {
+  return ((((r >> 1) ^ (r >> 3)) & 1) << 1) | ((r >> 2) & 1);
 }
 
-// Byte offset of logical (row, chunk) inside a tile with C chunks per row.
-template <int C>
+// Byte offset of logical (row, chunk) inside a tile of ROWS rows.
+template <int ROWS>
 __device__ __forceinline__ int tile_off(int row, int chunk) {
-  return (row * C + (chunk ^ swz<C>(row))) * 16;
+  return (chunk >> 2) * (ROWS * 64) + row * 64 + (((chunk & 3) ^ swz4(row)) << 4);
 }
 
 // DMA plan of a ROWS x C-chunk tile shared by NWAVE waves: wave-instruction i
@@ -61,6 +65,7 @@ struct Dma {
   static constexpr int N = ROWS * C / 64;              // instructions per tile
   static constexpr int PER_WAVE = (N + NWAVE - 1) / NWAVE;
   static_assert(ROWS * C % 64 == 0, "tile must be a whole number of 1 KB wave loads");
+  static_assert(C % 4 == 0 && ROWS % 16 == 0, "tile shape");
 
   uint32_t voff[PER_WAVE > 0 ? PER_WAVE : 1];
 
@@ -68,14 +73,19 @@ struct Dma {
   // (features / 8); chunks past it read zeros.
   __device__ __forceinline__ void init(int wave, int lane, uint32_t row_bytes, int valid_chunks) {
 #pragma unroll
-    for (int j = 0; j < PER_WAVE; ++j) {
-      const int i = wave + j * NWAVE;
-      const int p = 64 * i + lane;
-      const int row = p / C;
-      const int col = (p % C) ^ swz<C>(row);
-      voff[j] = (i < N && col < valid_chunks) ? (uint32_t)row * row_bytes + (uint32_t)col * 16u
-                                              : kOOB;
-    }
+    for (int j = 0; j < PER_WAVE; ++j)
+      voff[j] = slot_offset(wave + j * NWAVE, lane, row_bytes, valid_chunks);
+  }
+
+  // Global byte offset of the chunk that lands in slot 64 i + lane.
+  __device__ __forceinline__ static uint32_t slot_offset(int i, int lane, uint32_t row_bytes,
+                                                         int valid_chunks) {
+    const int p = 64 * i + lane;
+    const int grp = p / (ROWS * 4);
+    const int rem = p - grp * (ROWS * 4);
+    const int row = rem >> 2;
+    const int col = 4 * grp + ((rem & 3) ^ swz4(row));
+    return (i < N && col < valid_chunks) ? (uint32_t)row * row_bytes + (uint32_t)col * 16u : kOOB;
   }
 
   // Issue without a plan: the lane offsets are formed on the fly (for tiles
@@ -86,14 +96,10 @@ struct Dma {
 #pragma unroll
     for (int j = 0; j < PER_WAVE; ++j) {
       const int i = wave + j * NWAVE;
-      const int p = 64 * i + lane;
-      const int row = p / C;
-      const int col = (p % C) ^ swz<C>(row);
-      const uint32_t off = col < valid_chunks ? (uint32_t)row * row_bytes + (uint32_t)col * 16u
-                                              : kOOB;
       if (i < N)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(lds + i * 1024), 16, off, 0, 0,
-                                                 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (lds_void*)(lds + i * 1024), 16, slot_offset(i, lane, row_bytes, valid_chunks), 0,
+            0, 0);
     }
   }
 
@@ -109,35 +115,46 @@ struct Dma {
   }
 };
 
-// Row read: 8 bf16 of logical chunk `chunk` of row `row`.
-template <int C>
-__device__ __forceinline__ bf16x8 row_read(const uint8_t* tile, int row, int chunk) {
-  return as_bf16x8(*(const u32x4*)(tile + tile_off<C>(row, chunk)));
+// Per-lane offsets of row reads: lane reads row r0 + lane % 32 (r0 a
+// multiple of 16) at chunk 2s + lane / 32, the A operand of k-step s.
+struct RowLane {
+  int off[2];  // for even and odd s
+  __device__ __forceinline__ explicit RowLane(int lane) {
+    const int l = lane & 31, hl = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) off[j] = l * 64 + (((2 * j + hl) ^ swz4(l)) << 4);
+  }
+};
+
+// Row read: 8 bf16 of chunk 2s + lane / 32 of row r0 + lane % 32.
+template <int ROWS>
+__device__ __forceinline__ bf16x8 row_read(const uint8_t* tile, const RowLane& t, int r0, int s) {
+  return as_bf16x8(*(const u32x4*)(tile + (s >> 1) * (ROWS * 64) + r0 * 64 + t.off[s & 1]));
 }
 
-// Per-lane constants of a transpose read (see tr_operand).
+// Per-lane offsets of a transpose read: lane % 16 / 4 and lane / 32 pick the
+// row (0..7), (lane / 16) % 2 and lane % 4 / 2 the chunk in a column group,
+// lane % 2 the 8-byte half; the second read is 8 rows further down.
 struct TrLane {
-  int row;    // 4*(lane/32) + (lane%16)/4
-  int chunk;  // 2*((lane/16)%2) + (lane%4)/2
-  int byte;   // 8*(lane%2)
-  __device__ __forceinline__ explicit TrLane(int lane)
-      : row(4 * (lane >> 5) + ((lane & 15) >> 2)),
-        chunk(2 * ((lane >> 4) & 1) + ((lane & 3) >> 1)),
-        byte(8 * (lane & 1)) {}
+  int off0, off1;
+  __device__ __forceinline__ explicit TrLane(int lane) {
+    const int row = 4 * (lane >> 5) + ((lane & 15) >> 2);
+    const int chunk = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+    const int byte = 8 * (lane & 1);
+    off0 = row * 64 + ((chunk ^ swz4(row)) << 4) + byte;
+    off1 = (row + 8) * 64 + ((chunk ^ swz4(row + 8)) << 4) + byte;
+  }
 };
 
 // MFMA operand (32 x 16, lane % 32 <-> tile column m0 + lane % 32, k <-> 16
 // tile rows k0..k0+15 in the permuted order of an accumulator-built operand:
-// element e of lane-half h is row k0 + 8*(e/4) + 4*h + e%4) from a row-major
-// tile with C chunks per row.  Two ds_read_b64_tr_b16.
-template <int C>
+// element e of lane-half h is row k0 + 8*(e/4) + 4*h + e%4) from a tile of
+// ROWS rows; k0 a multiple of 16, m0 of 32.  Two ds_read_b64_tr_b16.
+template <int ROWS>
 __device__ __forceinline__ bf16x8 tr_operand(const uint8_t* tile, const TrLane& t, int k0, int m0) {
-  const int c = (m0 >> 3) + t.chunk;
-  const int r0 = k0 + t.row, r1 = k0 + 8 + t.row;
-  const v4i16 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_v4i16*)(tile + tile_off<C>(r0, c) + t.byte));
-  const v4i16 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_v4i16*)(tile + tile_off<C>(r1, c) + t.byte));
+  const uint8_t* base = tile + (m0 >> 5) * (ROWS * 64) + k0 * 64;
+  const v4i16 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(base + t.off0));
+  const v4i16 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(base + t.off1));
   typedef short v8i16 __attribute__((ext_vector_type(8)));
   const v8i16 ab = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
   return __builtin_bit_cast(bf16x8, ab);

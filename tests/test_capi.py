@@ -165,14 +165,20 @@ def test_fwd_and_bwd_entry_points_reject_before_gpu_work(lib):
     assert _capi.STATUS[lib.fna2_bwd(ctypes.byref(b), None)] == "FNA2_E_NULL"
 
 
-def test_bwd_workspace_is_small_and_rank_free(lib):
+def test_bwd_workspace_layout(lib):
     base = dict(dtype=1, varlen=0, batch=2, seqlen_q=256, seqlen_k=256, total_q=0, total_k=0,
                 heads=8, heads_kv=8, heads_graph=8, head_dim=128, causal=1, softmax_scale=0.1,
                 cu_seqlens_q=None, cu_seqlens_k=None)
     w32 = lib.fna2_bwd_workspace_bytes(ctypes.byref(_capi.Problem(rank=32, **base)))
     w64 = lib.fna2_bwd_workspace_bytes(ctypes.byref(_capi.Problem(rank=64, **base)))
-    # dense: fp32 d_graph_scale partials per (key tile, wave, graph head): 2 x 2 x 4 x 8
-    assert w32 == w64 == 2 * 2 * 4 * 8 * 4
+    w0 = lib.fna2_bwd_workspace_bytes(ctypes.byref(_capi.Problem(**{**base, "heads_graph": 0},
+                                                                 rank=0)))
+    rows = 2 * 256
+    partials = 4 * (2 * 2) * 4 * 8   # fp32 [query tiles][waves][graph heads]
+    nlse = rows * 8 * 4              # fp32 -LSE log2(e) per (row, head)
+    assert w32 == partials + rows * 8 * 32 * 2 + nlse  # + bf16(b Rq) at rank width 32
+    assert w64 == partials + rows * 8 * 64 * 2 + nlse
+    assert w0 == 256 + nlse                            # no graph heads: one aligned partial slot
 
 
 def test_python_errors_map_to_assertion(lib):
