@@ -1,0 +1,352 @@
+"""NaylisAttention on MI355X: the drop-in for ``FNA2/attention_fna2.py``.
+
+The module keeps the reference's constructor and ``forward`` signatures
+(attention_fna2.py:197-215, :380-390) and its backend choice
+(:220-233, :430-519, :533-617):
+
+* the FNA2 path -- dense (``x`` is ``[B, S, E]``) or varlen (``x`` is
+  ``[T, E]`` with ``cu_seqlens_q/k``) -- runs ``flash_naylis_attn``, i.e. the
+  gfx950 HIP kernels, with ``R_q``/``R_k`` of shape ``[B, H_G, S, R]`` /
+  ``[T, H_G, R]`` and ``graph_scale`` in fp32;
+* the paths the reference sends elsewhere keep going elsewhere: decode with a
+  KV cache, ``soft_cap`` and modules built with ``use_fna2=False`` use
+  PyTorch's SDPA with a materialised bias, or the explicit softmax when a
+  ``soft_cap`` or custom ``mask`` is given (attention_fna2.py:337-374,
+  :493-516).
+
+``_FNA2_AVAILABLE`` is true when the HIP library loads and the current device
+is gfx950.  A module asks for FNA2 with ``use_fna2=None`` (auto) or ``True``;
+as in the reference it is used when the rank is supported -- here any
+multiple of 8 up to 64 rather than only ``BLOCK_R`` (:225-229).  The FNA2 op
+itself never falls back: called without the library it raises.
+
+Varlen RoPE restarts positions at every sequence, as the reference's
+``_apply_rope_varlen`` (:620-647), with the positions formed on the device
+(no per-call host synchronisation).
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _capi
+from .flash_naylis_attn import BLOCK_R, flash_naylis_attn, rank_supported
+
+
+def _detect_fna2() -> bool:
+    if not torch.cuda.is_available():
+        return False
+    try:
+        _capi.lib()
+        arch = torch.cuda.get_device_properties(torch.cuda.current_device()).gcnArchName
+    except (OSError, RuntimeError, AttributeError):
+        return False
+    return arch.split(":")[0] == "gfx950"
+
+
+_FNA2_AVAILABLE = _detect_fna2()
+_FNA2_BLOCK_R = BLOCK_R
+_flash_naylis_attn = flash_naylis_attn
+
+KVCache = Tuple[torch.Tensor, torch.Tensor]
+
+
+class RMSNorm(nn.Module):
+    """y = x / sqrt(mean(x^2) + eps) * weight over the last dimension."""
+
+    def __init__(self, dim: int, eps: float = 1e-6):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        inv = torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + self.eps)
+        return x * inv * self.weight
+
+
+class RotaryPositionalEmbedding(nn.Module):
+    """Rotary embedding on the last dimension (two halves rotated), with the
+    optional YaRN frequency stretch of attention_fna2.py:129-142."""
+
+    def __init__(self, dim: int, max_seq_len: int = 2048, base: int = 10000,
+                 use_yarn: bool = False, yarn_scale: float = 1.0,
+                 yarn_original_max_len: int = 1024):
+        super().__init__()
+        self.dim = dim
+        self.max_seq_len = max_seq_len
+        self.base = base
+        self.use_yarn = use_yarn
+        self.yarn_scale = yarn_scale
+        self.yarn_original_max_len = yarn_original_max_len
+        half = torch.arange(0, dim, 2, dtype=torch.float32)
+        inv_freq = base ** (-half / dim)
+        if use_yarn and yarn_scale != 1.0:
+            # frequencies past the first max(dim/2, dim/4) even indices are
+            # divided by a factor rising linearly from 1 to yarn_scale
+            start = max(dim // 2, int(dim * 0.25))
+            ramp = 1 + (yarn_scale - 1) * (half - start) / (dim - start)
+            inv_freq = inv_freq / torch.where(half < start, torch.ones_like(half), ramp)
+        self.register_buffer("inv_freq", inv_freq)
+        self._cache_key = None
+        self._cos = self._sin = None
+
+    def _table(self, n: int, device, dtype):
+        key = (n, device, dtype)
+        if key != self._cache_key:
+            ang = torch.outer(torch.arange(n, device=device, dtype=dtype),
+                              self.inv_freq.to(device=device, dtype=dtype))
+            ang = torch.cat((ang, ang), dim=-1)
+            self._cos, self._sin, self._cache_key = ang.cos(), ang.sin(), key
+        return self._cos, self._sin
+
+    @staticmethod
+    def _rotate_half(x: torch.Tensor) -> torch.Tensor:
+        h = x.shape[-1] // 2
+        return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+    def rotate(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+        return x * cos + self._rotate_half(x) * sin
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor,
+                position_offset: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
+        s = q.shape[2]
+        cos, sin = self._table(s + position_offset, q.device, q.dtype)
+        cos = cos[position_offset:position_offset + s][None, None]
+        sin = sin[position_offset:position_offset + s][None, None]
+        return self.rotate(q, cos, sin), self.rotate(k, cos, sin)
+
+    def forward_varlen(self, q: torch.Tensor, k: torch.Tensor,
+                       cu_seqlens: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+        """q [T, H, D], k [T, H_KV, D]; position of token t = t - cu[seq(t)]."""
+        T = q.shape[0]
+        cu = cu_seqlens.to(device=q.device, dtype=torch.long)
+        t = torch.arange(T, device=q.device)
+        seq = torch.searchsorted(cu, t, right=True) - 1
+        pos = (t - cu[seq.clamp(min=0)]).clamp(min=0)
+        ang = torch.outer(pos.to(q.dtype), self.inv_freq.to(device=q.device, dtype=q.dtype))
+        ang = torch.cat((ang, ang), dim=-1)[:, None, :]
+        cos, sin = ang.cos(), ang.sin()
+        return self.rotate(q, cos, sin), self.rotate(k, cos, sin)
+
+
+class NaylisAttention(nn.Module):
+    """Token-graph attention: softmax(scale Q K^T + gs_h R_q R_k^T) V per head,
+    with R_q, R_k low-rank projections of x for the first H_G = num_heads -
+    vanilla_heads heads.  Constructor and forward as attention_fna2.py:197-215
+    and :380-390."""
+
+    def __init__(
+        self,
+        embed_dim: int,
+        num_heads: int,
+        dropout: float = 0.0,
+        use_rope: bool = True,
+        max_seq_len: int = 2048,
+        use_yarn: bool = False,
+        yarn_scale: float = 1.0,
+        yarn_original_max_len: int = 1024,
+        n_kv_heads: Optional[int] = None,
+        use_qk_norm: bool = True,
+        use_flash_attn: bool = True,
+        soft_cap: Optional[float] = None,
+        rel_rank: int = 32,
+        sym_heads: int = 0,
+        vanilla_heads: int = 0,
+        use_fna2: Optional[bool] = None,
+    ):
+        super().__init__()
+        assert embed_dim % num_heads == 0
+        graph_heads = num_heads - vanilla_heads
+        assert 0 <= sym_heads <= graph_heads
+        assert 0 <= vanilla_heads < num_heads
+
+        self._fna2_compatible = _FNA2_AVAILABLE and rank_supported(rel_rank)
+        want = (soft_cap is None) if use_fna2 is None else bool(use_fna2)
+        self._use_fna2 = want and self._fna2_compatible
+
+        self.embed_dim = embed_dim
+        self.num_heads = num_heads
+        self.head_dim = embed_dim // num_heads
+        self.use_rope = use_rope
+        self.use_qk_norm = use_qk_norm
+        self.soft_cap = soft_cap
+        self.rel_rank = rel_rank
+        self.sym_heads = sym_heads
+        self.vanilla_heads = vanilla_heads
+        self.graph_heads = graph_heads
+        self.n_kv_heads = num_heads if n_kv_heads is None else n_kv_heads
+        assert num_heads % self.n_kv_heads == 0
+        self.num_queries_per_kv = num_heads // self.n_kv_heads
+        self.kv_dim = self.n_kv_heads * self.head_dim
+
+        self.q_proj = nn.Linear(embed_dim, embed_dim, bias=False)
+        self.k_proj = nn.Linear(embed_dim, self.kv_dim, bias=False)
+        self.v_proj = nn.Linear(embed_dim, self.kv_dim, bias=False)
+        self.out_proj = nn.Linear(embed_dim, embed_dim, bias=False)
+        self.dropout = nn.Dropout(dropout)
+        if use_qk_norm:
+            self.q_norm = RMSNorm(self.head_dim)
+            self.k_norm = RMSNorm(self.head_dim)
+        else:
+            self.q_norm = self.k_norm = None
+        self.rope = (RotaryPositionalEmbedding(self.head_dim, max_seq_len, use_yarn=use_yarn,
+                                               yarn_scale=yarn_scale,
+                                               yarn_original_max_len=yarn_original_max_len)
+                     if use_rope else None)
+        if graph_heads > 0:
+            self.rel_q_proj = nn.Linear(embed_dim, graph_heads * rel_rank, bias=False)
+            self.rel_k_proj = nn.Linear(embed_dim, graph_heads * rel_rank, bias=False)
+            nn.init.normal_(self.rel_q_proj.weight, std=0.01)
+            nn.init.normal_(self.rel_k_proj.weight, std=0.01)
+            self.graph_scale = nn.Parameter(torch.zeros(graph_heads))
+        else:
+            self.rel_q_proj = self.rel_k_proj = None
+            self.graph_scale = None
+        self._sdpa_ok = hasattr(F, "scaled_dot_product_attention")
+
+    # ── helpers ────────────────────────────────────────────────────────────
+    def _attn_scale(self) -> float:
+        if self.rope is not None and self.rope.use_yarn and self.rope.yarn_scale > 1.0:
+            return math.sqrt(self.rope.yarn_scale) / math.sqrt(self.head_dim)
+        return 1.0 / math.sqrt(self.head_dim)
+
+    def _rel(self, x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+        """R_q, R_k in bf16: [B, H_G, S, R] from [B, S, E], or [T, H_G, R] from [T, E]."""
+        shape = x.shape[:-1] + (self.graph_heads, self.rel_rank)
+        r_q = self.rel_q_proj(x).view(shape).to(torch.bfloat16)
+        r_k = self.rel_k_proj(x).view(shape).to(torch.bfloat16)
+        if x.dim() == 3:
+            r_q, r_k = r_q.transpose(1, 2), r_k.transpose(1, 2)
+        return r_q.contiguous(), r_k.contiguous()
+
+    def _dense_bias(self, x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+        """gs_h R_q R_k^T for graph heads (zeros for vanilla heads), [B, H, S, S]."""
+        assert dtype == torch.bfloat16, "the graph bias is bf16"
+        B, S, _ = x.shape
+        r_q = self.rel_q_proj(x).view(B, S, self.graph_heads, self.rel_rank).transpose(1, 2)
+        r_k = self.rel_k_proj(x).view(B, S, self.graph_heads, self.rel_rank).transpose(1, 2)
+        bias = torch.matmul(r_q, r_k.transpose(-2, -1).contiguous())
+        if self.sym_heads > 0:
+            sym = bias[:, :self.sym_heads]
+            bias = torch.cat([(sym + sym.transpose(-2, -1)) * 0.5, bias[:, self.sym_heads:]], 1)
+        bias = (self.graph_scale.view(1, -1, 1, 1) * bias).to(dtype)
+        if self.vanilla_heads > 0:
+            bias = torch.cat([bias, bias.new_zeros(B, self.vanilla_heads, S, S)], dim=1)
+        return bias.contiguous()
+
+    def _finish(self, out: torch.Tensor, orig_dtype: torch.dtype) -> torch.Tensor:
+        if out.dtype != orig_dtype:
+            out = out.to(orig_dtype)
+        if out.dtype != self.out_proj.weight.dtype:
+            out = out.to(self.out_proj.weight.dtype)
+        return self.dropout(self.out_proj(out))
+
+    # ── forward ────────────────────────────────────────────────────────────
+    def forward(
+        self,
+        x: torch.Tensor,
+        mask: Optional[torch.Tensor] = None,
+        past_kv: Optional[KVCache] = None,
+        use_kv_cache: bool = False,
+        cu_seqlens_q: Optional[torch.Tensor] = None,
+        cu_seqlens_k: Optional[torch.Tensor] = None,
+        max_seqlen_q: Optional[int] = None,
+        max_seqlen_k: Optional[int] = None,
+    ) -> Tuple[torch.Tensor, Optional[KVCache]]:
+        if cu_seqlens_q is not None:
+            return self._forward_varlen(x, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                                        max_seqlen_k)
+        B, S, _ = x.shape
+        scale = self._attn_scale()
+        q = self.q_proj(x).view(B, S, self.num_heads, self.head_dim).transpose(1, 2)
+        k = self.k_proj(x).view(B, S, self.n_kv_heads, self.head_dim).transpose(1, 2)
+        v = self.v_proj(x).view(B, S, self.n_kv_heads, self.head_dim).transpose(1, 2)
+        if self.use_qk_norm:
+            q, k = self.q_norm(q), self.k_norm(k)
+        offset = past_kv[0].shape[2] if past_kv is not None else 0
+        if self.rope is not None:
+            q, k = self.rope(q, k, position_offset=offset)
+        if past_kv is not None:
+            k = torch.cat([past_kv[0], k], dim=2)
+            v = torch.cat([past_kv[1], v], dim=2)
+        new_cache: Optional[KVCache] = (k, v) if use_kv_cache else None
+
+        orig_dtype = q.dtype
+        if q.dtype == torch.float32:
+            q, k, v = (t.to(torch.bfloat16) for t in (q, k, v))
+        is_causal = S > 1 and past_kv is None
+        use_graph = self.graph_heads > 0 and (S > 1 or past_kv is None)
+
+        if self._use_fna2 and use_graph and self.soft_cap is None and past_kv is None:
+            r_q, r_k = self._rel(x)
+            out = _flash_naylis_attn(q, k, v, r_q, r_k, self.graph_scale.to(torch.float32),
+                                     softmax_scale=scale, is_causal=is_causal)
+        else:
+            out = self._attend_eager(x, q, k, v, mask, past_kv, scale, is_causal, use_graph)
+        out = out.transpose(1, 2).contiguous().view(B, S, self.embed_dim)
+        return self._finish(out, orig_dtype), new_cache
+
+    def _attend_eager(self, x, q, k, v, mask, past_kv, scale, is_causal, use_graph):
+        """The reference's non-FNA2 backends: SDPA with a dense bias, or the
+        explicit softmax for soft_cap (attention_fna2.py:449-516)."""
+        if self.n_kv_heads != self.num_heads:
+            k = k.repeat_interleave(self.num_queries_per_kv, dim=1)
+            v = v.repeat_interleave(self.num_queries_per_kv, dim=1)
+        p_drop = self.dropout.p if self.training else 0.0
+        bias = self._dense_bias(x, q.dtype) if use_graph else None
+        if self._sdpa_ok and self.soft_cap is None:
+            if bias is not None and is_causal:
+                sq, sk = q.shape[2], k.shape[2]
+                tri = torch.full((sq, sk), float("-inf"), device=q.device, dtype=q.dtype)
+                bias = bias + torch.triu(tri, diagonal=1 + (past_kv[0].shape[2] if past_kv else 0))
+            return F.scaled_dot_product_attention(
+                q, k, v, attn_mask=None if bias is None else bias.contiguous(),
+                is_causal=bias is None and is_causal, dropout_p=p_drop, scale=scale)
+        scores = torch.matmul(q, k.transpose(-2, -1)) * scale
+        if self.soft_cap is not None:
+            scores = self.soft_cap * torch.tanh(scores / self.soft_cap)
+        if bias is not None:
+            scores = scores + bias
+        if is_causal:
+            blocked = (mask.unsqueeze(0).unsqueeze(0) if mask is not None else
+                       torch.triu(torch.ones(q.shape[2], k.shape[2], device=q.device,
+                                             dtype=torch.bool), diagonal=1))
+            scores = scores.masked_fill(blocked, float("-inf"))
+        w = torch.nan_to_num(F.softmax(scores, dim=-1), nan=0.0)
+        if self.training and self.dropout.p > 0:
+            w = self.dropout(w)
+        return torch.matmul(w, v)
+
+    def _forward_varlen(self, x, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k):
+        """x [T, E] packed (attention_fna2.py:533-617); causal within each sequence."""
+        T = x.shape[0]
+        scale = self._attn_scale()
+        q = self.q_proj(x).view(T, self.num_heads, self.head_dim)
+        k = self.k_proj(x).view(T, self.n_kv_heads, self.head_dim)
+        v = self.v_proj(x).view(T, self.n_kv_heads, self.head_dim)
+        if self.use_qk_norm:
+            q, k = self.q_norm(q), self.k_norm(k)
+        if self.rope is not None:
+            q, k = self.rope.forward_varlen(q, k, cu_seqlens_q)
+        orig_dtype = q.dtype
+        if q.dtype == torch.float32:
+            q, k, v = (t.to(torch.bfloat16) for t in (q, k, v))
+        msq = max_seqlen_q if max_seqlen_q is not None else T
+        msk = max_seqlen_k if max_seqlen_k is not None else T
+        cu_k = cu_seqlens_k if cu_seqlens_k is not None else cu_seqlens_q
+        if not self._use_fna2:
+            raise RuntimeError("varlen NaylisAttention needs the FNA2 HIP kernels "
+                               "(gfx950 and libfna2_hip.so)")
+        if self.graph_heads > 0:
+            r_q, r_k = self._rel(x)
+            gs = self.graph_scale.to(torch.float32)
+        else:
+            r_q = r_k = gs = None
+        out = _flash_naylis_attn(q, k, v, r_q, r_k, gs, softmax_scale=scale, is_causal=True,
+                                 cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_k,
+                                 max_seqlen_q=msq, max_seqlen_k=msk)
+        return self._finish(out.reshape(T, self.embed_dim), orig_dtype), None

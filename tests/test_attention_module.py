@@ -1,0 +1,133 @@
+"""NaylisAttention drop-in (fna2_amd/attention_fna2.py).
+
+CPU: the constructor / forward signatures of the reference
+(FNA2/attention_fna2.py:197-215, :380-390), the device-side varlen RoPE
+against per-sequence RoPE, and the eager (non-FNA2) path.
+GPU: the FNA2 path (HIP kernels) against the module's eager SDPA path with the
+same weights, dense (GQA + vanilla heads) and packed varlen against the dense
+path run per sequence.
+"""
+import copy
+import inspect
+
+import pytest
+import torch
+
+from fna2_amd import attention_fna2 as A
+
+# FNA2/attention_fna2.py:197-215 and :380-390
+CTOR = [("embed_dim", inspect.Parameter.empty), ("num_heads", inspect.Parameter.empty),
+        ("dropout", 0.0), ("use_rope", True), ("max_seq_len", 2048), ("use_yarn", False),
+        ("yarn_scale", 1.0), ("yarn_original_max_len", 1024), ("n_kv_heads", None),
+        ("use_qk_norm", True), ("use_flash_attn", True), ("soft_cap", None),
+        ("rel_rank", 32), ("sym_heads", 0), ("vanilla_heads", 0), ("use_fna2", None)]
+FWD = [("x", inspect.Parameter.empty), ("mask", None), ("past_kv", None),
+       ("use_kv_cache", False), ("cu_seqlens_q", None), ("cu_seqlens_k", None),
+       ("max_seqlen_q", None), ("max_seqlen_k", None)]
+
+
+def _params(fn):
+    return [(n, p.default) for n, p in inspect.signature(fn).parameters.items() if n != "self"]
+
+
+def test_signatures_match_reference():
+    assert _params(A.NaylisAttention.__init__) == CTOR
+    assert _params(A.NaylisAttention.forward) == FWD
+    assert A._FNA2_BLOCK_R == 32
+
+
+def test_varlen_rope_equals_per_sequence_rope():
+    torch.manual_seed(0)
+    rope = A.RotaryPositionalEmbedding(64, max_seq_len=512)
+    lens = [5, 17, 1, 40]
+    cu = torch.tensor([0, 5, 22, 23, 63], dtype=torch.int32)
+    q = torch.randn(sum(lens), 4, 64)
+    k = torch.randn(sum(lens), 2, 64)
+    qo, ko = rope.forward_varlen(q, k, cu)
+    off = 0
+    for n in lens:
+        qs = q[off:off + n].transpose(0, 1)[None]
+        ks = k[off:off + n].transpose(0, 1)[None]
+        qr, kr = rope(qs, ks)
+        torch.testing.assert_close(qo[off:off + n], qr[0].transpose(0, 1), atol=1e-5, rtol=1e-5)
+        torch.testing.assert_close(ko[off:off + n], kr[0].transpose(0, 1), atol=1e-5, rtol=1e-5)
+        off += n
+
+
+def test_yarn_scale_and_frequencies():
+    plain = A.RotaryPositionalEmbedding(64)
+    yarn = A.RotaryPositionalEmbedding(64, use_yarn=True, yarn_scale=4.0)
+    # even indices up to max(dim/2, dim/4) = 32 keep their frequency (the ramp
+    # starts at 1 there); above it the divisor rises linearly to yarn_scale
+    torch.testing.assert_close(yarn.inv_freq[:17], plain.inv_freq[:17])
+    assert torch.all(yarn.inv_freq[17:] < plain.inv_freq[17:])
+    torch.testing.assert_close(plain.inv_freq[31] / yarn.inv_freq[31],
+                               torch.tensor(1 + 3 * 30 / 32))
+    m = A.NaylisAttention(256, 4, use_yarn=True, yarn_scale=4.0)
+    assert abs(m._attn_scale() - 2.0 / 8.0) < 1e-12
+
+
+def test_eager_path_on_cpu_is_causal_attention():
+    torch.manual_seed(1)
+    m = A.NaylisAttention(128, 4, rel_rank=8, use_fna2=False).eval()
+    with torch.no_grad():
+        m.graph_scale.fill_(0.7)
+    x = torch.randn(2, 9, 128)
+    y, cache = m(x, use_kv_cache=True)
+    assert y.shape == (2, 9, 128) and cache[0].shape == (2, 4, 9, 32)
+    # causality: output at position t ignores later tokens
+    x2 = x.clone()
+    x2[:, 5:] += 1.0
+    y2, _ = m(x2)
+    torch.testing.assert_close(y[:, :5], y2[:, :5], atol=1e-5, rtol=1e-5)
+
+
+# ── GPU: the FNA2 path against the module's own eager path ──────────────────
+# The eager reference (bf16 SDPA with a dense bias, and its backward) runs on
+# the CPU; only the FNA2 copy runs on the GPU.
+
+def _pair(**kw):
+    torch.manual_seed(3)
+    ref = A.NaylisAttention(use_fna2=False, **kw)
+    with torch.no_grad():
+        ref.graph_scale.uniform_(0.5, 1.5)
+    fast = copy.deepcopy(ref).cuda()
+    fast._use_fna2 = True
+    return ref, fast
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kw", [
+    dict(embed_dim=512, num_heads=8, rel_rank=32),
+    dict(embed_dim=512, num_heads=4, n_kv_heads=2, rel_rank=16, vanilla_heads=1),
+])
+def test_fna2_path_matches_eager_dense(gpu, kw):
+    assert A._FNA2_AVAILABLE
+    ref, fast = _pair(**kw)
+    x = torch.randn(2, 200, kw["embed_dim"])
+    y_ref, _ = ref(x)
+    y_fast, _ = fast(x.cuda())
+    assert (y_fast.cpu() - y_ref).abs().max().item() < 2e-2
+    g = torch.randn_like(y_ref)
+    gr = torch.autograd.grad(y_ref, list(ref.parameters()), g)
+    gf = torch.autograd.grad(y_fast, list(fast.parameters()), g.cuda())
+    for (name, _), a, b in zip(ref.named_parameters(), gr, gf):
+        b = b.cpu()
+        rel = ((a - b).float().norm() / a.float().norm().clamp_min(1e-6)).item()
+        assert rel < 5e-2, (name, rel)
+
+
+@pytest.mark.gpu
+def test_fna2_varlen_matches_dense_per_sequence(gpu):
+    _, fast = _pair(embed_dim=512, num_heads=8, rel_rank=32)
+    lens = [37, 128, 5, 90]
+    x = torch.randn(sum(lens), 512, device="cuda")
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32,
+                      device="cuda")
+    y, _ = fast(x, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=max(lens),
+                max_seqlen_k=max(lens))
+    off = 0
+    for n in lens:
+        yd, _ = fast(x[off:off + n][None])
+        assert (y[off:off + n] - yd[0]).abs().max().item() < 2e-2
+        off += n
