@@ -46,7 +46,141 @@ def parse():
                     help="approximate CPU-baseline budget (seconds)")
     ap.add_argument("--no-flush", action="store_true",
                     help="skip the cache-flushed measurement")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device-to-device copy (the known-size kernel that "
+                         "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE) and print its rate")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("WORKLOAD_DIR", "COPY_DIR"),
+                    help="turn rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this bench and "
+                         "of --copy-calibration into profiles/traffic_<config>.json")
+    ap.add_argument("--summarize-trace", nargs=3, metavar=("DB_DIR", "OUT_MD", "COMMAND"),
+                    help="write the rocprofv3 --kernel-trace --stats table of DB_DIR to OUT_MD")
+    ap.add_argument("--summarize-counters", nargs=3, metavar=("DB_DIR", "OUT_MD", "COMMAND"),
+                    help="write the per-kernel means of a rocprofv3 --pmc pass to OUT_MD")
     return ap.parse_args()
+
+
+COPY_BYTES = 1 << 30
+TRAFFIC_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+
+
+def copy_calibration():
+    """1 GiB device copy, 10 times: reads and writes exactly COPY_BYTES per launch."""
+    import torch
+
+    x = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        y.copy_(x)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / 10
+    print(json.dumps({"copy_bytes": COPY_BYTES, "ms": round(ms, 4),
+                      "GBps_read_plus_write": round(2 * COPY_BYTES / ms / 1e6, 1)}), flush=True)
+
+
+def _profiler_rows(d, query):
+    """Rows of `query` over every rocprofv3 database (*_results.db) under d."""
+    import glob
+    import sqlite3
+    rows = []
+    for fn in sorted(glob.glob(os.path.join(d, "**", "*_results.db"), recursive=True)):
+        con = sqlite3.connect(fn)
+        try:
+            rows += con.execute(query).fetchall()
+        finally:
+            con.close()
+    return rows
+
+
+def _short(name):
+    return name.replace("(anonymous namespace)::", "").split("(")[0]
+
+
+def _pmc_means(d):
+    """Mean counter value (KiB per dispatch, summed over XCDs) per kernel name."""
+    acc = {}
+    for name, ctr, v in _profiler_rows(
+            d, "select kernel_name, counter_name, value from counters_collection"):
+        acc.setdefault((_short(name), ctr), []).append(float(v))
+    return {k: sum(v) / len(v) for k, v in acc.items()}
+
+
+def summarize_trace(d, out_md, command):
+    """Markdown table of rocprofv3 --kernel-trace --stats (the top_kernels view)."""
+    rows = _profiler_rows(d, "select name, total_calls, total_duration, average, percentage "
+                             "from top_kernels order by total_duration desc")
+    lines = [f"Command: `{command}`", "",
+             "| kernel | calls | total (us) | average (us) | % of GPU time |",
+             "|---|---|---|---|---|"]
+    for name, calls, tot, avg, pct in rows:
+        lines.append(f"| `{_short(name)}` | {calls} | {tot:.1f} | {avg:.2f} | {pct:.1f} |")
+    with open(out_md, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def summarize_counters(d, out_md, command):
+    """Markdown table of the mean counter values per kernel (one --pmc pass)."""
+    m = _pmc_means(d)
+    ctrs = sorted({c for _, c in m})
+    kernels = sorted({k for k, _ in m if k.startswith("fna2::")})
+    lines = [f"Command: `{command}`", "", "Mean per dispatch (summed over the XCDs).", "",
+             "| kernel | " + " | ".join(ctrs) + " |", "|---" * (len(ctrs) + 1) + "|"]
+    for k in kernels:
+        lines.append(f"| `{k}` | " + " | ".join(f"{m.get((k, c), float('nan')):.4g}"
+                                                for c in ctrs) + " |")
+    with open(out_md, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def summarize_pmc(work_dir, copy_dir, config):
+    """Calibrated HBM bytes per launch.  Each counter is scaled by the factor
+    that makes the copy kernel's reading equal its known size (1 GiB read and
+    1 GiB written per launch)."""
+    w, c = _pmc_means(work_dir), _pmc_means(copy_dir)
+    copy_fetch = max(v for (n, k), v in c.items() if k == "FETCH_SIZE" and "copyBuffer" in n)
+    copy_write = max(v for (n, k), v in c.items() if k == "WRITE_SIZE" and "copyBuffer" in n)
+    f_fetch = COPY_BYTES / (copy_fetch * 1024.0)
+    f_write = COPY_BYTES / (copy_write * 1024.0)
+    kernels = {}
+    for (name, ctr), v in w.items():
+        if not name.startswith("fna2::"):
+            continue
+        short = name.split("::")[-1]
+        e = kernels.setdefault(short, {})
+        if ctr == "FETCH_SIZE":
+            e["fetch_bytes"] = round(v * 1024.0 * f_fetch)
+        elif ctr == "WRITE_SIZE":
+            e["write_bytes"] = round(v * 1024.0 * f_write)
+    out = {"config": config, "calibration": {"fetch_factor": round(f_fetch, 4),
+                                             "write_factor": round(f_write, 4),
+                                             "copy_bytes": COPY_BYTES},
+           "kernels": kernels}
+    path = os.path.join(TRAFFIC_DIR, f"traffic_{config}.json")
+    with open(path, "w") as fh:
+        json.dump(out, fh, indent=1)
+        fh.write("\n")
+    print(json.dumps(out), flush=True)
+
+
+def measured_traffic(config, kernel):
+    """HBM bytes per launch of `kernel` from profiles/traffic_<config>.json, or None."""
+    key = {"fwd": "fwd_kernel", "dkdv": "dkdv_kernel", "dq": "dq_kernel"}[kernel]
+    try:
+        with open(os.path.join(TRAFFIC_DIR, f"traffic_{config}.json")) as fh:
+            ks = json.load(fh)["kernels"]
+    except (OSError, ValueError, KeyError):
+        return None
+    for name, e in ks.items():
+        if name.startswith(key) and "fetch_bytes" in e and "write_bytes" in e:
+            return e["fetch_bytes"] + e["write_bytes"]
+    return None
 
 
 def kernel_bytes(cfg, name):
@@ -143,6 +277,18 @@ def cpu_baseline(cfg, inp, budget_s):
 
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration()
+        return
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc, args.config)
+        return
+    if args.summarize_trace:
+        summarize_trace(*args.summarize_trace)
+        return
+    if args.summarize_counters:
+        summarize_counters(*args.summarize_counters)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build runs the "
               "kernels on a single MI355X; multi-GPU sharding is described in DESIGN.md and "
@@ -235,7 +381,10 @@ def main():
         ach = nflops / dur_s / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4)}
-    roof["traffic"] = None
+    roof["traffic"] = measured_traffic(cfg.name, dom)
+    roof["traffic_source"] = (f"profiles/traffic_{cfg.name}.json (rocprofv3 FETCH_SIZE + "
+                              "WRITE_SIZE per dispatch, copy-calibrated)"
+                              if roof["traffic"] is not None else None)
     roof["kernel"] = dom
     roof["algorithmic_bytes"] = nbytes
     roof["algorithmic_flops"] = nflops
