@@ -5,29 +5,40 @@
 //
 // Persistent: one workgroup per CU walks a list of work items, an item being
 // the 128 keys of one key tile of one KV head; workgroup g takes items
-// g, 2G-1-g, 2G+g, ... (snake order over a longest-first list).  Wave w owns
-// keys 32w..32w+31 of the item and keeps K | Rk and V rows in registers (the
-// B operands of S = Qa Ka^T and dP = dO V^T, one key per lane).  For each
-// query head of the GQA group the item walks the 64-query blocks that can
-// see its keys (causal: from the key tile's diagonal on).  Per block:
-//   S, dP      (64 x 32 per wave)       A operands: Q | bf16(b Rq) and dO rows
-//   P  = exp(S - LSE),  dS = P (dP - delta)
-//   dV^T  += dO^T P                    A operand: dO^T by transpose reads
-//   acc^T += [Q | bf16(b Rq)]^T dS     A operand: the same tiles transposed
-// and the epilogue writes dK = a c acc_D, dRk = c acc_R (acc_R built from the
-// rank operand bf16(b Rq), so c acc_R = graph_scale dS^T Rq).  The dQ kernel
-// stores that operand, rounded exactly as the forward rounds it, with delta
-// and -LSE log2(e); the sign/zero factor a of the augmented query rides on the
-// stationary K (exact), so the recomputed S equals the forward's bit for bit.  dK and dV
-// accumulate over the whole GQA group in fp32 registers: no atomics.
+// g, 2G-1-g, 2G+g, ... (snake order over a longest-first list).  For each
+// query head of the GQA group an item walks the 32-query blocks that can see
+// its keys (causal: from the key tile's diagonal on).
 //
-// Q, bf16(b Rq), dO, -LSE log2(e) and delta tiles stream in by DMA through a three-stage ring
-// that runs two blocks ahead of the compute across item boundaries, so the
-// next item's first tiles are in flight while the current item finishes.  At
-// an item's last block, once its MFMAs are issued, the epilogue stores go out
-// and the next item's K | Rk, V rows are loaded into the stationary
-// registers.  The stages are separate LDS objects and the loop is unrolled by
-// three so that the compiler can prove reads and in-flight DMA never alias.
+// The workgroup's 8 waves split the work by role, two waves per SIMD:
+//   * producer wave w (0-3) keeps the K | Rk and V rows of keys 32w..32w+31
+//     in registers (B operands, one key per lane) and per block forms
+//       S, dP  (32 x 32)               A operands: Q | bf16(b Rq) and dO rows
+//       P = exp(S - LSE),  dS = P (dP - delta)
+//     and stores P and dS, already in MFMA operand layout, to LDS;
+//   * consumer wave 4 + w holds the fp32 accumulators of the same keys and,
+//     one block behind, forms
+//       dV^T  += dO^T P                A operand: dO^T by transpose reads
+//       acc^T += [Q | bf16(b Rq)]^T dS A operand: the same tiles transposed
+//     and at the end of an item writes dK = a c acc_D, dRk = c acc_R (acc_R
+//     is built from the rank operand bf16(b Rq), so c acc_R = graph_scale
+//     dS^T Rq) and dV.
+// A producer's softmax arithmetic thus overlaps its SIMD partner's MFMAs,
+// and neither role needs more than half of the SIMD's registers.  dK and dV
+// accumulate over the whole GQA group in fp32: no atomics.
+//
+// The dQ kernel stores the rank operand bf16(b Rq), rounded exactly as the
+// forward rounds it, together with delta and -LSE log2(e); the sign/zero
+// factor a of the augmented query rides on the stationary K (exact), so the
+// recomputed S equals the forward's bit for bit.
+//
+// Q, bf16(b Rq), dO, -LSE log2(e) and delta tiles stream in by DMA (issued by
+// the producers) through a four-stage ring that runs two blocks ahead of the
+// producers, across item boundaries; the consumers read a stage one block
+// later.  At the first block of an (item, head) the producers start loading
+// the rows of the next one into a second register set.  Both roles meet at
+// one barrier per block.  The stages are separate LDS objects and the loops
+// are unrolled by four so that the compiler can prove that reads and
+// in-flight DMA never alias.
 #include "fna2_kernels.h"
 #include "fna2_tile.h"
 
@@ -37,9 +48,11 @@ namespace {
 
 template <int D, int RPL>
 struct KvCfg {
-  static constexpr int NW = 4;
-  static constexpr int BN = kKvBN;  // keys per item
-  static constexpr int BM = kKvBM;  // queries per block
+  static constexpr int NP = 4;       // producer waves (as many consumers)
+  static constexpr int NW = 2 * NP;  // waves per workgroup
+  static constexpr int BN = kKvBN;   // keys per item
+  static constexpr int BM = kKvBM;   // queries per block
+  static_assert(BM == 32 && BN == 32 * NP, "one 32 x 32 MFMA block per wave");
   static constexpr int CD = D / 8;
   static constexpr int CR = RPL > 0 ? RPL / 8 : 4;
   static constexpr int KSD = D / 16;
@@ -49,18 +62,58 @@ struct KvCfg {
   static constexpr int QB = BM * D * 2;
   static constexpr int RB = BM * RPL * 2;
   static constexpr int OB = BM * D * 2;
-  static constexpr int LB = 4 * BM * 4;  // LSE, delta, two scratch rows
+  static constexpr int LB = 2 * 256;  // -LSE log2(e), delta: one 64-lane dword DMA each
   static constexpr int STAGE = QB + RB + OB + LB;
+  static constexpr int PW = 4 * 1024;  // a producer's P and dS operands of one block
+  static constexpr int PDS = NP * PW;
   static constexpr int ERS = D * 2 + 16;  // epilogue staging row stride (bytes)
-  // DMA instructions each wave issues per block (LSE/delta: one dword load).
-  static constexpr int PER_STEP = 2 * Dma<BM, CD, NW>::PER_WAVE +
-                                  (RPL > 0 ? Dma<BM, CR, NW>::PER_WAVE : 0) + 1;
+  static constexpr int N_KV = 2 * KSD + KSR;  // stationary-row loads of an item
+  using DmaD = Dma<BM, CD, NP>;
+  using DmaR = Dma<BM, CR, NP>;
+  // VMEM instructions every producer wave issues per block (Q, dO, rank
+  // operand, one -LSE log2(e) / delta row), the same for every wave.
+  static constexpr int NB = 2 * DmaD::PER_WAVE + (RPL > 0 ? DmaR::PER_WAVE : 0) + 1;
 };
 
+// Scheduling pattern for a region of n MFMAs that each consume `per` LDS
+// reads: `ahead` MFMAs' reads are issued first, then one MFMA and the reads
+// of a later one alternate.  This bounds the registers held by operands in
+// flight (the scheduler would otherwise hoist every read).
+template <int N, int PER, int AHEAD>
+__device__ __forceinline__ void pipe_lds_mfma() {
+#pragma unroll
+  for (int i = 0; i < AHEAD; ++i) __builtin_amdgcn_sched_group_barrier(0x100, PER, 0);
+#pragma unroll
+  for (int i = 0; i < N - AHEAD; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, PER, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < AHEAD; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+}
+
+// The kernel's parameter block, re-read where it is used: the pointer is
+// made opaque, so the loads are not hoisted out of the loops and the values
+// are not held (or spilled) across them.  Used on the per-item paths only.
+typedef const __attribute__((address_space(4))) BwdParams* ParamsPtr;
+__device__ __forceinline__ ParamsPtr params_here() {
+  ParamsPtr pp = (ParamsPtr)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(pp));
+  return pp;
+}
+__device__ __forceinline__ TView view_of(const __attribute__((address_space(4))) TView* v) {
+  TView t;
+  t.ptr = v->ptr;
+  t.sb = v->sb;
+  t.ss = v->ss;
+  t.sh = v->sh;
+  return t;
+}
+
 struct KvItem {
-  int tix, b, kvh, k0t;  // key tile index, sequence, KV head, first key
+  int b, kvh, k0t;  // sequence, KV head, first key of the tile
   SeqExt e;
-  int qb_lo, nqb;        // first query block that sees the tile; blocks per head
+  int qb_lo, nqb;   // first query block that sees the tile; blocks per head
 };
 
 // Position in a workgroup's program: item (round r), head hi, block qi.
@@ -76,26 +129,31 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
   __shared__ __attribute__((aligned(1024))) uint8_t st0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t st1[C::STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t st2[C::STAGE];
-  __shared__ __attribute__((aligned(16))) uint8_t epi[C::NW * 32 * C::ERS];
+  __shared__ __attribute__((aligned(1024))) uint8_t st3[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t pd0[C::PDS];
+  __shared__ __attribute__((aligned(1024))) uint8_t pd1[C::PDS];
+  __shared__ __attribute__((aligned(16))) uint8_t epi[C::NP * 32 * C::ERS];
   const Problem& p = P.p;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = uni(tid >> 6);
+  const int kw = wv & (C::NP - 1);  // key slice of this wave
   const int l32 = lane & 31, hl = lane >> 5;
-  const int krow = wv * 32 + l32;  // this lane's key within the item
+  const int krow = kw * 32 + l32;   // this lane's key within the item
   const int G = gridDim.x, g = blockIdx.x;
   const int n_items =
-      (P.tiles_k ? uni(*P.n_tiles_k) : p.nseq * cdiv(p.sk, C::BN)) * p.H_KV;
+      (P.tiles_k ? uni(*const_space(P.n_tiles_k)) : p.nseq * cdiv(p.sk, C::BN)) * p.H_KV;
 
-  auto decode = [&](int w) {
+  auto decode = [&](int r) {
     KvItem x;
-    x.tix = w / p.H_KV;
-    x.kvh = w - x.tix * p.H_KV;
+    const int w = r * G + ((r & 1) ? G - 1 - g : g);
+    const int tix = w / p.H_KV;
+    x.kvh = w - tix * p.H_KV;
     int kt;
     if (P.tiles_k) {
-      tile_decode(P.tiles_k, x.tix, x.b, kt, x.e);
+      tile_decode(P.tiles_k, tix, x.b, kt, x.e);
     } else {
-      x.b = x.tix % p.nseq;
-      kt = x.tix / p.nseq;
+      x.b = tix % p.nseq;
+      kt = tix / p.nseq;
       x.e = seq_ext_uniform(p, x.b);
     }
     x.k0t = kt * C::BN;
@@ -103,348 +161,438 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     x.nqb = max(cdiv(x.e.lq, C::BM) - x.qb_lo, 0);
     return x;
   };
+  auto round_valid = [&](int r) { return r * G + ((r & 1) ? G - 1 - g : g) < n_items; };
 
-  f32x16 dvacc[C::NDB];
-  f32x16 dkacc[C::NDB + C::NRB];
-  bf16x8 kreg[C::KSD + C::KSR];
-  bf16x8 vreg[C::KSD];
-
-  // Stationary rows of item x (B operands): lane holds key row krow,
-  // features 16s + 8hl .. +7 for step s.  The streamed Q tile is raw, so the
-  // factor a in {1, -1, 0} of the augmented operand goes on K (exact).
-  const uint32_t kxor = p.qa < 0.f ? 0x80008000u : 0u;
-  const uint32_t kand = p.qa == 0.f ? 0u : 0xffffffffu;
-  auto load_kv = [&](const KvItem& x) {
-    const uint32_t krows = (uint32_t)max(min(C::BN, x.e.lk - x.k0t), 0);
-    const uint32_t krb = (uint32_t)P.k.ss * 2u, vrb = (uint32_t)P.v.ss * 2u;
-    const uint16_t* kb = seq_base<const uint16_t>(P.k, p, x.b, x.e.k0, x.kvh);
-    const uint16_t* vb = seq_base<const uint16_t>(P.v, p, x.b, x.e.k0, x.kvh);
-    const auto rk = make_rsrc(kb + (int64_t)x.k0t * P.k.ss, krows * krb);
-    const auto rv = make_rsrc(vb + (int64_t)x.k0t * P.v.ss, krows * vrb);
-    const uint32_t ko = (uint32_t)krow * krb + 16u * hl;
-    const uint32_t vo = (uint32_t)krow * vrb + 16u * hl;
-#pragma unroll
-    for (int s = 0; s < C::KSD; ++s) {
-      kreg[s] = as_bf16x8(__builtin_amdgcn_raw_buffer_load_b128(rk, ko + 32u * s, 0, 0));
-      vreg[s] = as_bf16x8(__builtin_amdgcn_raw_buffer_load_b128(rv, vo + 32u * s, 0, 0));
-    }
-    // (a = 1, the usual case, needs no transform, so nothing here waits for
-    // the loads.)
-    if (p.qa != 1.f) {
-#pragma unroll
-      for (int s = 0; s < C::KSD; ++s) {
-        u32x4 kv = as_u32x4(kreg[s]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kv[i] = (kv[i] & kand) ^ kxor;
-        kreg[s] = as_bf16x8(kv);
-      }
-    }
-  };
-  // Rank part of the stationary K operand for query head h (raw Rk).
-  auto load_rk = [&](const KvItem& x, int h) {
-    if constexpr (C::KSR > 0) {
-      const bool graph = h < p.H_G;
-      const uint32_t krows = (uint32_t)max(min(C::BN, x.e.lk - x.k0t), 0);
-      const uint32_t rrb = (uint32_t)P.rk.ss * 2u;
-      const uint16_t* rkb = graph ? seq_base<const uint16_t>(P.rk, p, x.b, x.e.k0, h)
-                                  : (const uint16_t*)P.rk.ptr;
-      const auto rr = make_rsrc(rkb + (int64_t)x.k0t * P.rk.ss, graph ? krows * rrb : 0u);
-      const uint32_t ro = (uint32_t)krow * rrb + 16u * hl;
-#pragma unroll
-      for (int s = 0; s < C::KSR; ++s) {
-        const bool in = (2 * s + hl) * 8 < p.R;
-        kreg[C::KSD + s] =
-            as_bf16x8(__builtin_amdgcn_raw_buffer_load_b128(rr, in ? ro + 32u * s : kOOB, 0, 0));
-      }
-    }
-  };
-
-  // Per head: dRk = c acc_R (acc_R = dS^T bf16(b Rq) and b c = graph_scale).
-  // zero: an item no query block sees.
-  auto write_drk = [&](const KvItem& x, int h, bool zero) {
-    if constexpr (C::NRB > 0) {
-      const int key = x.k0t + krow;
-      if (h < p.H_G && key < x.e.lk) {
-        const float sr = zero ? 0.f : p.c;
-        uint16_t* rrow = seq_base<uint16_t>(P.drk, p, x.b, x.e.k0, h) + (int64_t)key * P.drk.ss;
-#pragma unroll
-        for (int f = 0; f < C::NRB; ++f)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int rf = f * 32 + 8 * q + 4 * hl;
-            if (rf < p.R) {
-              const f32x16& a = dkacc[C::NDB + f];
-              u32x2 val;
-              val[0] = zero ? 0u : pack_bf16(sr * a[4 * q], sr * a[4 * q + 1]);
-              val[1] = zero ? 0u : pack_bf16(sr * a[4 * q + 2], sr * a[4 * q + 3]);
-              *(u32x2*)(rrow + rf) = val;
-            }
-          }
-      }
-    }
-  };
-  // dK = a c acc_D and dV: each wave stages its 32 rows through its own LDS
-  // buffer so that a store instruction writes whole rows (4 rows of 16-byte
-  // chunks for d = 128), instead of 64 scattered 8-byte pieces.
-  uint8_t* obuf = epi + wv * 32 * C::ERS;
-  auto write_rows = [&](const KvItem& x, const f32x16* acc, float sc, bool zero,
-                        const TView& out) {
-#pragma unroll
-    for (int d = 0; d < C::NDB; ++d)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        u32x2 val;
-        val[0] = zero ? 0u : pack_bf16(sc * acc[d][4 * q], sc * acc[d][4 * q + 1]);
-        val[1] = zero ? 0u : pack_bf16(sc * acc[d][4 * q + 2], sc * acc[d][4 * q + 3]);
-        *(u32x2*)(obuf + l32 * C::ERS + (d * 32 + 8 * q + 4 * hl) * 2) = val;
-      }
-    constexpr int CPR = D / 8;       // 16-byte chunks per row
-    constexpr int RPI = 64 / CPR;    // rows per store instruction
-    uint16_t* base = seq_base<uint16_t>(out, p, x.b, x.e.k0, x.kvh);
-#pragma unroll
-    for (int i = 0; i < 32 / RPI; ++i) {
-      const int r = i * RPI + lane / CPR, ch = lane % CPR;
-      const u32x4 v = *(const u32x4*)(obuf + r * C::ERS + ch * 16);
-      const int key = x.k0t + wv * 32 + r;
-      if (key < x.e.lk) st16(base + (int64_t)key * out.ss + ch * 8, v);
-    }
-  };
-  auto write_dkdv = [&](const KvItem& x, bool zero) {
-    write_rows(x, dkacc, p.qa * p.c, zero, P.dk);
-    write_rows(x, dvacc, 1.f, zero, P.dv);
-  };
-
-  // ---- the program: items in snake order, then heads, then blocks ----
-  // An item no query block can see (keys past every query under the causal
-  // mask, or an empty query range) has zero gradients; the compute cursor
-  // writes them as it passes.
-  auto next_item = [&](KvCursor& c, bool compute) {
+  // The program: items in snake order, then the heads of the GQA group, then
+  // 32-query blocks.  An item no query block can see (keys past every query
+  // under the causal mask, or an empty query range) has zero gradients;
+  // on_zero is called as the cursor passes it.
+  auto next_item = [&](KvCursor& c, auto&& on_zero) {
     for (;;) {
       ++c.r;
-      const int w = c.r * G + ((c.r & 1) ? G - 1 - g : g);
-      if (w >= n_items) {
+      if (!round_valid(c.r)) {
         c.done = true;
         return;
       }
-      c.it = decode(w);
+      c.it = decode(c.r);
       c.hi = 0;
       c.qi = 0;
       if (c.it.nqb > 0) return;
-      if (compute) {
-        write_dkdv(c.it, true);
-        for (int hi = 0; hi < p.group; ++hi) write_drk(c.it, c.it.kvh * p.group + hi, true);
-      }
+      on_zero(c.it);
     }
   };
-  auto advance = [&](KvCursor& c, bool compute) {
+  auto advance = [&](KvCursor& c, auto&& on_zero) {
     if (++c.qi < c.it.nqb) return;
     c.qi = 0;
     if (++c.hi < p.group) return;
-    next_item(c, compute);
+    next_item(c, on_zero);
+  };
+  auto start = [&](KvCursor& c, auto&& on_zero) {
+    c.r = -1;
+    c.done = false;
+    next_item(c, on_zero);
+  };
+  auto no_zero = [](const KvItem&) {};
+  // Whether this wave's 32 keys meet block qi of the cursor's item.
+  auto block_active = [&](const KvCursor& c) {
+    const int wk0 = c.it.k0t + kw * 32;
+    const int qbase = (c.it.qb_lo + c.qi) * C::BM;
+    return wk0 < c.it.e.lk && (!p.causal || qbase + C::BM - 1 >= wk0);
   };
 
-  // DMA plans for the streamed tiles.
-  const uint32_t qrb = (uint32_t)P.q.ss * 2u, orb = (uint32_t)P.dout.ss * 2u;
-  const uint32_t srb = (uint32_t)P.rqs.ss * 2u;
-  Dma<C::BM, C::CD, C::NW> dmq, dmo;
-  Dma<C::BM, C::CR, C::NW> dmr;
-  dmq.init(wv, lane, qrb, C::CD);
-  dmo.init(wv, lane, orb, C::CD);
-  if constexpr (RPL > 0) dmr.init(wv, lane, srb, C::CR);
-  const uint32_t lrb = (uint32_t)P.nlse.ss * 4u, drb = (uint32_t)P.delta.ss * 4u;
-  const bool is_delta = (wv & 1) != 0;                                 // waves 1, 3: delta
-  const int lslot = (wv & 1) * C::BM * 4 + (wv >> 1) * 2 * C::BM * 4;  // 2, 3: scratch rows
-  const uint32_t loff = (uint32_t)lane * (is_delta ? drb : lrb);
+  if (wv < C::NP) {
+    // ============================ producers ============================
+    const RowLane rdl(lane);
+    const uint32_t qrb = (uint32_t)P.q.ss * 2u, orb = (uint32_t)P.dout.ss * 2u;
+    const uint32_t srb = (uint32_t)P.rqs.ss * 2u;
+    typename C::DmaD dmq, dmo;
+    typename C::DmaR dmr;
+    dmq.init_fixed(wv, lane, qrb, C::CD);
+    dmo.init_fixed(wv, lane, orb, C::CD);
+    if constexpr (RPL > 0) dmr.init_fixed(wv, lane, srb, C::CR);
+    // Waves 0 and 2 fetch the -LSE log2(e) row of a block, 1 and 3 the delta
+    // row (the same bytes twice: every wave issues as many instructions).
+    const bool is_delta = (wv & 1) != 0;
+    const uint32_t lrb = (uint32_t)P.nlse.ss * 4u, drb = (uint32_t)P.delta.ss * 4u;
+    const uint32_t loff = (uint32_t)lane * (is_delta ? drb : lrb);
 
-  auto issue = [&](const KvCursor& c, uint8_t* st) {
-    const KvItem& x = c.it;
-    const int h = x.kvh * p.group + c.hi;
-    const int qbase = (x.qb_lo + c.qi) * C::BM;
-    const uint32_t rows = (uint32_t)max(min(C::BM, x.e.lq - qbase), 0);
-    const uint16_t* qb = seq_base<const uint16_t>(P.q, p, x.b, x.e.q0, h);
-    const uint16_t* ob = seq_base<const uint16_t>(P.dout, p, x.b, x.e.q0, h);
-    dmq.issue(make_rsrc(qb + (int64_t)qbase * P.q.ss, rows * qrb), st, wv);
-    if constexpr (RPL > 0) {
+    // Buffer descriptors for the issue cursor's (item, head), set when it
+    // enters one: they span the sequence's whole query range, so rows past
+    // it read as zeros, and a block only adds its row offset to the lane
+    // offsets.  (The host keeps a sequence's rows under 2 GB.)
+    u32x4 sq, so, sr, sl;
+    auto setup = [&](const KvCursor& c) {
+      if (c.done) {  // past the last block: the ring's last DMAs read nothing
+        sq = rsrc_words(P.q.ptr, 0u);
+        so = sq;
+        sr = sq;
+        sl = sq;
+        return;
+      }
+      const KvItem& x = c.it;
+      const int h = x.kvh * p.group + c.hi;
+      const uint32_t lq = (uint32_t)x.e.lq;
+      const ParamsPtr pp = params_here();
+      const uint16_t* qb = seq_base<const uint16_t>(view_of(&pp->q), p, x.b, x.e.q0, h);
+      sq = rsrc_words(qb, lq * qrb);
+      so = rsrc_words(seq_base<const uint16_t>(view_of(&pp->dout), p, x.b, x.e.q0, h), lq * orb);
+      if constexpr (RPL > 0) {
+        const bool graph = h < p.H_G;
+        sr = rsrc_words(graph ? seq_base<const uint16_t>(view_of(&pp->rqs), p, x.b, x.e.q0, h) : qb,
+                        graph ? lq * srb : 0u);
+      }
+      const float* lb = seq_base<const float>(is_delta ? view_of(&pp->delta) : view_of(&pp->nlse),
+                                              p, x.b, x.e.q0, h);
+      sl = rsrc_words(lb, lq * (is_delta ? drb : lrb));
+    };
+    // Exactly C::NB VMEM instructions, unconditionally.
+    auto issue = [&](const KvCursor& c, uint8_t* st) {
+      const uint32_t q0 = c.done ? 0u : (uint32_t)((c.it.qb_lo + c.qi) * C::BM);
+      dmq.issue_fixed(sq, st, wv, q0 * qrb);
+      if constexpr (RPL > 0) dmr.issue_fixed(sr, st + C::QB, wv, q0 * srb);
+      dmo.issue_fixed(so, st + C::QB + C::RB, wv, q0 * orb);
+      dma_lds<4>(sl, lds_addr(st + C::QB + C::RB + C::OB + (is_delta ? 256 : 0)),
+                 loff + q0 * (is_delta ? drb : lrb));
+    };
+    // Stationary rows (B operands): lane holds key krow, features
+    // 16s + 8hl .. +7 of k-step s: K | Rk and V of the producer's (item,
+    // head), loaded in place (load16_inplace) and waited for by the ring
+    // barrier.  Rank chunks past R are read as they come and zeroed once the
+    // loads have completed.
+    u32x4 kreg[C::KSD + C::KSR], vreg[C::KSD];
+#pragma unroll
+    for (int s = 0; s < C::KSD + C::KSR; ++s) kreg[s] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int s = 0; s < C::KSD; ++s) vreg[s] = u32x4{0u, 0u, 0u, 0u};
+    auto load_rows = [&](const KvItem& x, int h) {
+      const ParamsPtr pp = params_here();
+      const TView vk = view_of(&pp->k), vv = view_of(&pp->v), vr = view_of(&pp->rk);
+      const uint32_t krows = (uint32_t)max(min(C::BN, x.e.lk - x.k0t), 0);
+      const uint32_t krb = (uint32_t)vk.ss * 2u, vrb = (uint32_t)vv.ss * 2u;
+      const uint32_t rrb = (uint32_t)vr.ss * 2u;
       const bool graph = h < p.H_G;
-      const uint16_t* sb = graph ? seq_base<const uint16_t>(P.rqs, p, x.b, x.e.q0, h) : qb;
-      dmr.issue(make_rsrc(sb + (int64_t)qbase * P.rqs.ss, graph ? rows * srb : 0u), st + C::QB,
-                wv);
-    }
-    dmo.issue(make_rsrc(ob + (int64_t)qbase * P.dout.ss, rows * orb), st + C::QB + C::RB, wv);
-    const float* lb = is_delta ? seq_base<const float>(P.delta, p, x.b, x.e.q0, h)
-                               : seq_base<const float>(P.nlse, p, x.b, x.e.q0, h);
-    const int64_t lss = is_delta ? P.delta.ss : P.nlse.ss;
-    const auto rl = make_rsrc(lb + (int64_t)qbase * lss, rows * (is_delta ? drb : lrb));
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rl, (lds_void*)(st + C::QB + C::RB + C::OB + lslot), 4, loff, 0, 0, 0);
-  };
-
-  const TrLane tl(lane);
-  const RowLane rdl(lane);
-
-  auto compute = [&](const KvCursor& c, const uint8_t* cur) {
-    const KvItem& x = c.it;
-    const int h = x.kvh * p.group + c.hi;
-    const bool graph = (RPL > 0) && (h < p.H_G);
-    const int key = x.k0t + krow;
-    const int wk0 = x.k0t + wv * 32;
-    const int qbase = (x.qb_lo + c.qi) * C::BM;
-    const bool active = wk0 < x.e.lk && (!p.causal || qbase + C::BM - 1 >= wk0);
-    if (!active) return;
-    const bool diag = p.causal && wk0 + 31 > qbase;
-    const uint8_t* qt = cur;
-    const uint8_t* rt = cur + C::QB;
-    const uint8_t* ot = cur + C::QB + C::RB;
-    const float* ls = (const float*)(cur + C::QB + C::RB + C::OB);
-    const int nrs = graph ? cdiv(p.R, 16) : 0;
-    bf16x8 pb[2][2], db[2][2];
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      f32x16 sacc = f32x16{}, dpacc = f32x16{};
-#pragma unroll
-      for (int s = 0; s < C::KSD; ++s) sacc = mfma32(row_read<C::BM>(qt, rdl, rb * 32, s), kreg[s], sacc);
-      if constexpr (C::KSR > 0) {
+      const uint16_t* kb = seq_base<const uint16_t>(vk, p, x.b, x.e.k0, x.kvh);
+      const uint16_t* vb = seq_base<const uint16_t>(vv, p, x.b, x.e.k0, x.kvh);
+      const uint16_t* rkb = graph ? seq_base<const uint16_t>(vr, p, x.b, x.e.k0, h) : kb;
+      const u32x4 rk = rsrc_words(kb + (int64_t)x.k0t * vk.ss, krows * krb);
+      const u32x4 rv = rsrc_words(vb + (int64_t)x.k0t * vv.ss, krows * vrb);
+      const u32x4 rr = rsrc_words(rkb + (int64_t)x.k0t * vr.ss, graph ? krows * rrb : 0u);
+      const uint32_t ko = (uint32_t)krow * krb + 16u * hl;
+      const uint32_t vo = (uint32_t)krow * vrb + 16u * hl;
+      const uint32_t ro = (uint32_t)krow * rrb + 16u * hl;
+      static_for<C::KSD>([&](auto s) {
+        load16_inplace<32 * decltype(s)::value>(kreg[s], rk, ko);
+        load16_inplace<32 * decltype(s)::value>(vreg[s], rv, vo);
+      });
+      static_for<C::KSR>([&](auto s) {
+        load16_inplace<32 * decltype(s)::value>(kreg[C::KSD + s], rr, ro);
+      });
+    };
+    auto mask_rk = [&]() {
+      if (C::KSR > 0 && (p.R & 15) != 0) {
 #pragma unroll
         for (int s = 0; s < C::KSR; ++s)
-          if (s < nrs)
-            sacc = mfma32(row_read<C::BM>(rt, rdl, rb * 32, s),
-                          kreg[C::KSD + s], sacc);
+          if ((2 * s + hl) * 8 >= p.R) kreg[C::KSD + s] = u32x4{0u, 0u, 0u, 0u};
+      }
+    };
+    // The streamed Q tile is raw, so the factor a in {1, -1, 0} of the
+    // augmented operand goes on K (exact): Q (a K)^T = (a Q) K^T.
+    const uint32_t kxor = p.qa < 0.f ? 0x80008000u : 0u;
+    const uint32_t kand = p.qa == 0.f ? 0u : 0xffffffffu;
+    auto sign_k = [&]() {
+      if (p.qa != 1.f) {
+#pragma unroll
+        for (int s = 0; s < C::KSD; ++s)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) kreg[s][i] = (kreg[s][i] & kand) ^ kxor;
+      }
+    };
+
+    // S and dP of this wave's 32 keys against block qi of the cursor.
+    auto scores = [&](const KvCursor& c, const uint8_t* cur, f32x16& sacc, f32x16& dpacc) {
+      // (A vanilla head, or rank padding, has zero rank operands: its rank
+      // MFMAs add exact zeros and keep the block one basic block.)
+      const uint8_t* qt = cur;
+      const uint8_t* rt = cur + C::QB;
+      const uint8_t* ot = cur + C::QB + C::RB;
+      // All A operands are read first (the LDS latency is paid once per
+      // block, not once per MFMA); S and dP chains interleave.
+      bf16x8 qa[C::KSD + C::KSR], oa[C::KSD];
+#pragma unroll
+      for (int s = 0; s < C::KSD; ++s) qa[s] = row_read<C::BM>(qt, rdl, 0, s);
+#pragma unroll
+      for (int s = 0; s < C::KSR; ++s) qa[C::KSD + s] = row_read<C::BM>(rt, rdl, 0, s);
+#pragma unroll
+      for (int s = 0; s < C::KSD; ++s) oa[s] = row_read<C::BM>(ot, rdl, 0, s);
+      sacc = f32x16{};
+      dpacc = f32x16{};
+#pragma unroll
+      for (int s = 0; s < C::KSD; ++s) {
+        sacc = mfma32(qa[s], as_bf16x8(kreg[s]), sacc);
+        dpacc = mfma32(oa[s], as_bf16x8(vreg[s]), dpacc);
       }
 #pragma unroll
-      for (int s = 0; s < C::KSD; ++s) dpacc = mfma32(row_read<C::BM>(ot, rdl, rb * 32, s), vreg[s], dpacc);
-      // P and dS for rows rb*32 + 8g + 4hl + j (accumulator register 4g + j).
+      for (int s = 0; s < C::KSR; ++s) sacc = mfma32(qa[C::KSD + s], as_bf16x8(kreg[C::KSD + s]), sacc);
+      // issue order: every read, then every MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * C::KSD + C::KSR, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * C::KSD + C::KSR, 0);
+    };
+    // P = exp(S - LSE) and dS = P (dP - delta) to LDS in the B-operand layout
+    // of the consumer's MFMAs: for k-half j (query rows 16j..16j+15), lane
+    // (key l32, half hl) holds rows 16j + 8i + 4hl + e, i = 0..1, e = 0..3,
+    // i.e. accumulator registers 8j..8j+7.
+    auto softmax = [&](const KvCursor& c, const uint8_t* cur, uint8_t* pd, const f32x16& sacc,
+                       const f32x16& dpacc) {
+      const KvItem& x = c.it;
+      const int qbase = (x.qb_lo + c.qi) * C::BM;
+      const float* ls = (const float*)(cur + C::QB + C::RB + C::OB);
       // Zero-filled query rows (past the sequence) have Q = dO = LSE =
-      // delta = 0 and so P (dP - delta) = 0: only the causal diagonal needs
-      // a mask; columns of keys past the sequence are never stored.
-      if (diag) {
+      // delta = 0, so P (dP - delta) = 0 there; columns of keys past the
+      // sequence are never stored.  Only the causal diagonal needs a mask:
+      // query row qbase + r sees key k0t + krow iff r >= thr.
+      const int thr = (p.causal && x.k0t + kw * 32 + 31 > qbase) ? x.k0t + krow - qbase
+                                                                  : -(1 << 30);
+      u32x4 pk[2], dk[2];
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int q = qbase + rb * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
-          sacc[v] = key <= q ? sacc[v] : kNegInf;
+      for (int gq = 0; gq < 4; ++gq) {
+        const int r0 = 8 * gq + 4 * hl;
+        const f32x4_t nl4 = *(const f32x4_t*)(ls + r0);
+        const f32x4_t dl4 = *(const f32x4_t*)(ls + 64 + r0);
+        float pv[4], dv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int v = 4 * gq + j;
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[v], p.c2, nl4[j]));
+          pv[j] = r0 + j >= thr ? e : 0.f;
+          dv[j] = pv[j] * (dpacc[v] - dl4[j]);
         }
+        pk[gq >> 1][2 * (gq & 1)] = pack_bf16(pv[0], pv[1]);
+        pk[gq >> 1][2 * (gq & 1) + 1] = pack_bf16(pv[2], pv[3]);
+        dk[gq >> 1][2 * (gq & 1)] = pack_bf16(dv[0], dv[1]);
+        dk[gq >> 1][2 * (gq & 1) + 1] = pack_bf16(dv[2], dv[3]);
       }
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        u32x4 pk, dk;
-#pragma unroll
-        for (int g2 = 0; g2 < 2; ++g2) {
-          const int g = 2 * half + g2;
-          const int r0 = rb * 32 + 8 * g + 4 * hl;
-          const f32x4_t lse4 = *(const f32x4_t*)(ls + r0);  // -LSE log2(e)
-          const f32x4_t dl4 = *(const f32x4_t*)(ls + C::BM + r0);
-          float pv[4], dv[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int v = 4 * g + j;
-            pv[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[v], p.c2, lse4[j]));
-            dv[j] = pv[j] * (dpacc[v] - dl4[j]);
-          }
-          pk[2 * g2] = pack_bf16(pv[0], pv[1]);
-          pk[2 * g2 + 1] = pack_bf16(pv[2], pv[3]);
-          dk[2 * g2] = pack_bf16(dv[0], dv[1]);
-          dk[2 * g2 + 1] = pack_bf16(dv[2], dv[3]);
-        }
-        pb[rb][half] = as_bf16x8(pk);
-        db[rb][half] = as_bf16x8(dk);
-      }
+      uint8_t* o = pd + kw * C::PW + lane * 16;
+      st16(o, pk[0]);
+      st16(o + 1024, pk[1]);
+      st16(o + 2048, dk[0]);
+      st16(o + 3072, dk[1]);
+    };
+
+    // The ring: every step issues exactly C::NB VMEM instructions (the DMA
+    // of block T + 2), so "wait until C::NB are in flight" at step T's
+    // barrier waits for block T's tiles and everything issued before them,
+    // and nothing newer.  The rows of the next (item, head) are loaded by
+    // the last block of the current one, after its MFMAs and before its DMA,
+    // so the next step's barrier also waits for them.  The DMA and the row
+    // loads are inline assembly, so the compiler adds no wait of its own.
+    KvCursor pc;  // the block being produced
+    start(pc, no_zero);
+    KvCursor ic = pc;  // the block whose tiles are issued next (two ahead)
+    setup(ic);
+    if (!pc.done) load_rows(pc.it, pc.it.kvh * p.group + pc.hi);
+    issue(ic, st0);
+    if (!ic.done) {
+      advance(ic, no_zero);
+      if (ic.done || ic.qi == 0) setup(ic);
     }
-    // dV^T += dO^T P ; dKa^T += Qa^T dA
+    issue(ic, st1);
+    if (!ic.done) {
+      advance(ic, no_zero);
+      if (ic.done || ic.qi == 0) setup(ic);
+    }
+
+    // Block T (stage `cur`): wait for its tiles; S, dP; at the last block of
+    // an (item, head), load the next one's rows into the registers just
+    // read; start the DMA of block T + 2; P, dS.
+    auto step = [&](const uint8_t* cur, uint8_t* nxt, uint8_t* pd) {
+      ring_barrier<C::NB>();
+      if (pc.done) return;
+      if (pc.qi == 0) {  // rows loaded by the previous block (or above)
+        sign_k();
+        mask_rk();
+      }
+      KvCursor nx = pc;
+      advance(nx, no_zero);
+      const bool act = block_active(pc);
+      f32x16 sacc, dpacc;
+      __builtin_amdgcn_sched_barrier(0);
+      if (act) scores(pc, cur, sacc, dpacc);
+      __builtin_amdgcn_sched_barrier(0);
+      if (!nx.done && nx.qi == 0) load_rows(nx.it, nx.it.kvh * p.group + nx.hi);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(ic, nxt);
+      if (!ic.done) {
+        advance(ic, no_zero);
+        if (ic.done || ic.qi == 0) setup(ic);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (act) softmax(pc, cur, pd, sacc, dpacc);
+      __builtin_amdgcn_sched_barrier(0);
+      pc = nx;
+    };
+    // Block T uses stage T % 4 and P/dS buffer T % 2.  Steps 0 .. nblocks-1
+    // produce; one more meets the consumers' last barrier.
+    for (;;) {
+      bool last = pc.done;
+      step(st0, st2, pd0);
+      if (last) break;
+      last = pc.done;
+      step(st1, st3, pd1);
+      if (last) break;
+      last = pc.done;
+      step(st2, st0, pd0);
+      if (last) break;
+      last = pc.done;
+      step(st3, st1, pd1);
+      if (last) break;
+    }
+  } else {
+    // ============================ consumers ============================
+    const TrLane tl(lane);
+    f32x16 dvacc[C::NDB];
+    f32x16 dkacc[C::NDB + C::NRB];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int i = 0; i < C::NDB; ++i) dvacc[i] = f32x16{};
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int k0 = rb * 32 + 16 * half;
+    for (int i = 0; i < C::NDB + C::NRB; ++i) dkacc[i] = f32x16{};
+
+    // dRk of head h = c acc_R (zero: an item no query block sees).
+    auto write_drk = [&](const KvItem& x, int h, bool zero) {
+      if constexpr (C::NRB > 0) {
+        const int key = x.k0t + krow;
+        if (h < p.H_G && key < x.e.lk) {
+          const float sr = zero ? 0.f : p.c;
+          const TView vd = view_of(&params_here()->drk);
+          uint16_t* rrow = seq_base<uint16_t>(vd, p, x.b, x.e.k0, h) + (int64_t)key * vd.ss;
+#pragma unroll
+          for (int f = 0; f < C::NRB; ++f)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int rf = f * 32 + 8 * q + 4 * hl;
+              if (rf < p.R) {
+                const f32x16& a = dkacc[C::NDB + f];
+                u32x2 val;
+                val[0] = zero ? 0u : pack_bf16(sr * a[4 * q], sr * a[4 * q + 1]);
+                val[1] = zero ? 0u : pack_bf16(sr * a[4 * q + 2], sr * a[4 * q + 3]);
+                *(u32x2*)(rrow + rf) = val;
+              }
+            }
+        }
+      }
+    };
+    // dK = a c acc_D and dV: each wave stages its 32 rows through its own LDS
+    // buffer so that a store instruction writes whole rows.
+    uint8_t* obuf = epi + kw * 32 * C::ERS;
+    auto write_rows = [&](const KvItem& x, const f32x16* acc, float sc, bool zero,
+                          const TView& out) {
+#pragma unroll
+      for (int d = 0; d < C::NDB; ++d)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          u32x2 val;
+          val[0] = zero ? 0u : pack_bf16(sc * acc[d][4 * q], sc * acc[d][4 * q + 1]);
+          val[1] = zero ? 0u : pack_bf16(sc * acc[d][4 * q + 2], sc * acc[d][4 * q + 3]);
+          *(u32x2*)(obuf + l32 * C::ERS + (d * 32 + 8 * q + 4 * hl) * 2) = val;
+        }
+      constexpr int CPR = D / 8;     // 16-byte chunks per row
+      constexpr int RPI = 64 / CPR;  // rows per store instruction
+      uint16_t* base = seq_base<uint16_t>(out, p, x.b, x.e.k0, x.kvh);
+#pragma unroll
+      for (int i = 0; i < 32 / RPI; ++i) {
+        const int r = i * RPI + lane / CPR, ch = lane % CPR;
+        const u32x4 v = *(const u32x4*)(obuf + r * C::ERS + ch * 16);
+        const int key = x.k0t + kw * 32 + r;
+        if (key < x.e.lk) st16(base + (int64_t)key * out.ss + ch * 8, v);
+      }
+    };
+    auto write_dkdv = [&](const KvItem& x, bool zero) {
+      const ParamsPtr pp = params_here();
+      write_rows(x, dkacc, p.qa * p.c, zero, view_of(&pp->dk));
+      write_rows(x, dvacc, 1.f, zero, view_of(&pp->dv));
+    };
+    auto on_zero = [&](const KvItem& x) {
+      write_dkdv(x, true);
+      for (int hi = 0; hi < p.group; ++hi) write_drk(x, x.kvh * p.group + hi, true);
+    };
+
+    // (acc_R of a vanilla head is built from zero tiles and never stored.)
+    auto consume = [&](const uint8_t* cur, const uint8_t* pd) {
+      const uint8_t* qt = cur;
+      const uint8_t* rt = cur + C::QB;
+      const uint8_t* ot = cur + C::QB + C::RB;
+      const uint8_t* o = pd + kw * C::PW + lane * 16;
+      bf16x8 pb[2], db[2];
+      pb[0] = as_bf16x8(ld16(o));
+      pb[1] = as_bf16x8(ld16(o + 1024));
+      db[0] = as_bf16x8(ld16(o + 2048));
+      db[1] = as_bf16x8(ld16(o + 3072));
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
 #pragma unroll
         for (int d = 0; d < C::NDB; ++d)
-          dvacc[d] = mfma32(tr_operand<C::BM>(ot, tl, k0, 32 * d), pb[rb][half], dvacc[d]);
+          dvacc[d] = mfma32(tr_operand<C::BM>(ot, tl, 16 * j, 32 * d), pb[j], dvacc[d]);
 #pragma unroll
-        for (int f = 0; f < C::NDB; ++f)
-          dkacc[f] = mfma32(tr_operand<C::BM>(qt, tl, k0, 32 * f), db[rb][half], dkacc[f]);
-        if constexpr (C::NRB > 0) {
-          if (graph) {
+        for (int d = 0; d < C::NDB; ++d)
+          dkacc[d] = mfma32(tr_operand<C::BM>(qt, tl, 16 * j, 32 * d), db[j], dkacc[d]);
 #pragma unroll
-            for (int f = 0; f < C::NRB; ++f)
-              dkacc[C::NDB + f] =
-                  mfma32(tr_operand<C::BM>(rt, tl, k0, 32 * f), db[rb][half], dkacc[C::NDB + f]);
-          }
-        }
+        for (int f = 0; f < C::NRB; ++f)
+          dkacc[C::NDB + f] =
+              mfma32(tr_operand<C::BM>(rt, tl, 16 * j, 32 * f), db[j], dkacc[C::NDB + f]);
       }
-  };
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      pipe_lds_mfma<2 * (2 * C::NDB + C::NRB), 2, 3>();
+    };
 
-  KvCursor cc;  // compute cursor
-  cc.r = -1;
-  cc.done = false;
-  next_item(cc, true);
-  if (cc.done) return;
-  load_kv(cc.it);
-  load_rk(cc.it, cc.it.kvh * p.group);
+    KvCursor cc;  // the block being consumed
+    start(cc, on_zero);
+    // Step t consumes block t - 1 (nothing at t = 0).  The barrier does not
+    // wait for the consumers' own stores.
+    bool first = true;
+    auto step = [&](const uint8_t* cur, const uint8_t* pd) {
+      ring_barrier<63>();
+      if (first) {
+        first = false;
+        return;
+      }
+      if (cc.done) return;
+      if (block_active(cc)) consume(cur, pd);
+      if (cc.qi + 1 < cc.it.nqb) {
+        ++cc.qi;
+        return;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      const KvItem x = cc.it;
+      const bool last_head = cc.hi + 1 == p.group;
+      write_drk(x, x.kvh * p.group + cc.hi, false);
+      if (last_head) write_dkdv(x, false);
 #pragma unroll
-  for (int i = 0; i < C::NDB; ++i) dvacc[i] = f32x16{};
+      for (int i = C::NDB; i < C::NDB + C::NRB; ++i) dkacc[i] = f32x16{};
+      if (last_head) {
 #pragma unroll
-  for (int i = 0; i < C::NDB + C::NRB; ++i) dkacc[i] = f32x16{};
-
-  KvCursor ic = cc;  // issue cursor, two blocks ahead
-  int pending = 1;
-  issue(ic, st0);
-  advance(ic, false);
-  if (!ic.done) {
-    issue(ic, st1);
-    advance(ic, false);
-    ++pending;
-  }
-
-  // One block: wait for its tiles, start the DMA two blocks ahead into
-  // `nxt`, compute on `cur`; after an item's (head's) last block, write its
-  // results and load the next item's (head's) stationary rows.
-  auto step = [&](const uint8_t* cur, uint8_t* nxt) {
-    if (pending == 2) ring_barrier<C::PER_STEP>(); else ring_barrier<0>();
-    --pending;
-    if (!ic.done) {
-      issue(ic, nxt);
-      advance(ic, false);
-      ++pending;
+        for (int i = 0; i < C::NDB; ++i) dvacc[i] = f32x16{};
+#pragma unroll
+        for (int i = 0; i < C::NDB; ++i) dkacc[i] = f32x16{};
+      }
+      advance(cc, on_zero);
+    };
+    // Stage and P/dS buffer of block t - 1: st[(t + 3) % 4], pd[(t + 1) % 2].
+    for (;;) {
+      step(st3, pd1);
+      if (cc.done) break;
+      step(st0, pd0);
+      if (cc.done) break;
+      step(st1, pd1);
+      if (cc.done) break;
+      step(st2, pd0);
+      if (cc.done) break;
     }
-    __builtin_amdgcn_sched_barrier(0);
-    compute(cc, cur);
-    if (cc.qi + 1 < cc.it.nqb) {
-      ++cc.qi;
-      return;
-    }
-    // Keep the stores and the next item's loads after this block's MFMAs (the
-    // old and new stationary rows must not be live at once).
-    __builtin_amdgcn_sched_barrier(0);
-    const KvItem x = cc.it;
-    const bool last_head = cc.hi + 1 == p.group;
-    write_drk(x, x.kvh * p.group + cc.hi, false);
-    if (last_head) write_dkdv(x, false);
-    advance(cc, true);
-    if (cc.done) return;
-    if (last_head) {
-      load_kv(cc.it);
-#pragma unroll
-      for (int i = 0; i < C::NDB; ++i) dvacc[i] = f32x16{};
-#pragma unroll
-      for (int i = 0; i < C::NDB; ++i) dkacc[i] = f32x16{};
-    }
-    load_rk(cc.it, cc.it.kvh * p.group + cc.hi);
-#pragma unroll
-    for (int i = C::NDB; i < C::NDB + C::NRB; ++i) dkacc[i] = f32x16{};
-  };
-
-  for (;;) {
-    step(st0, st2);
-    if (cc.done) break;
-    step(st1, st0);
-    if (cc.done) break;
-    step(st2, st1);
-    if (cc.done) break;
   }
 }
 
 // One non-template kernel per (D, padded rank) so that each has a host stub.
-#define FNA2_DKDV_KERNEL(D, RPL)                                                    \
-  __global__ __launch_bounds__(256, 1) void dkdv_kernel_d##D##_r##RPL(const BwdParams P) { \
-    dkdv_body<D, RPL>(P);                                                           \
+#define FNA2_DKDV_KERNEL(D, RPL)                                                      \
+  __global__ __launch_bounds__(512, 1) void dkdv_kernel_d##D##_r##RPL(const BwdParams P) { \
+    dkdv_body<D, RPL>(P);                                                             \
   }
 FNA2_DKDV_KERNEL(64, 0)
 FNA2_DKDV_KERNEL(64, 32)
@@ -464,7 +612,7 @@ hipError_t launch_bwd_dkdv(const BwdParams& P, int rpl, int grid, hipStream_t s)
   if (P.p.D == 128)
     k = rpl == 0 ? dkdv_kernel_d128_r0 : rpl == 32 ? dkdv_kernel_d128_r32 : dkdv_kernel_d128_r64;
   if (!k || (rpl != 0 && rpl != 32 && rpl != 64)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k, dim3(grid), dim3(256), 0, s, P);
+  hipLaunchKernelGGL(k, dim3(grid), dim3(512), 0, s, P);
   return hipGetLastError();
 }
 

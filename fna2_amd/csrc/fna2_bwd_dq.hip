@@ -53,7 +53,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   int b, qt;
   SeqExt e;
   if (P.tiles_q) {
-    if (tix >= uni(*P.n_tiles_q)) return;
+    if (tix >= uni(*const_space(P.n_tiles_q))) return;
     tile_decode(P.tiles_q, tix, b, qt, e);
   } else {
     const int nqt = cdiv(p.sq, C::BM);

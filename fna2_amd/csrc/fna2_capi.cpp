@@ -148,11 +148,11 @@ BwdWs bwd_ws(const fna2_problem& p) {
   // d_gs partials: [query tiles][4 waves][H_G]
   off += align_up(sizeof(float) * 4u * (size_t)(g.q_tiles > 0 ? g.q_tiles : 1) *
                   (size_t)(p.heads_graph > 0 ? p.heads_graph : 1));
-  // bf16(graph_scale / c * Rq), [rows_q][H_G][rank width]
+  // bf16(graph_scale / c * Rq), [H_G][rows_q][rank width] (per batch)
   w.rqs = off;
   const int rpl = fna2::padded_rank32(p.heads_graph, p.rank);
   off += align_up((size_t)rows_q(p) * (size_t)p.heads_graph * (size_t)rpl * 2u);
-  // -LSE log2(e), fp32 [rows_q][H]
+  // -LSE log2(e), fp32 [H][rows_q] (per batch)
   w.nlse = off;
   off += align_up((size_t)rows_q(p) * (size_t)p.heads * 4u);
   w.bytes = off;
@@ -299,6 +299,14 @@ int fna2_check_bwd(const fna2_bwd_args* a) {
   FNA2_TRY(check_view(a->r_k, p, kw && g, true, 2));
   FNA2_TRY(check_view(a->dr_k, p, kw && g, true, 2));
   if (g && (!a->graph_scale || !a->d_graph_scale)) return FNA2_E_NULL;
+  // The dK/dV kernel addresses one sequence's query rows of a head with
+  // 32-bit byte offsets.
+  auto span_ok = [&](const fna2_tensor& t, uint64_t esize) {
+    const uint64_t ss = (uint64_t)(t.stride_s < 0 ? -t.stride_s : t.stride_s);
+    return (uint64_t)p.seqlen_q * ss * esize < (1ull << 31);
+  };
+  if (qw && !(span_ok(a->q, 2) && span_ok(a->dout, 2) && span_ok(a->delta, 4)))
+    return FNA2_E_SHAPE;
   const BwdWs w = bwd_ws(p);
   if (a->workspace_bytes < w.bytes || !a->workspace) return FNA2_E_WORKSPACE;
   return FNA2_OK;
@@ -379,14 +387,17 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
   const Grids g = grids(p);
   K.dgs_partial = (float*)((char*)a->workspace + w.partial);
   const int rpl = fna2::padded_rank32(K.p.H_G, K.p.R);
+  // Both are head-major (a head's rows are contiguous): the dK/dV kernel
+  // reads them per head, 32 rows at a time.
+  const int64_t seq_rows = p.varlen ? (int64_t)p.total_q : (int64_t)p.seqlen_q;
   K.rqs.ptr = (char*)a->workspace + w.rqs;
-  K.rqs.sh = rpl;
-  K.rqs.ss = (int64_t)p.heads_graph * rpl;
-  K.rqs.sb = p.varlen ? 0 : (int64_t)p.seqlen_q * K.rqs.ss;
+  K.rqs.ss = rpl;
+  K.rqs.sh = seq_rows * rpl;
+  K.rqs.sb = p.varlen ? 0 : (int64_t)p.heads_graph * K.rqs.sh;
   K.nlse.ptr = (char*)a->workspace + w.nlse;
-  K.nlse.sh = 1;
-  K.nlse.ss = p.heads;
-  K.nlse.sb = p.varlen ? 0 : (int64_t)p.seqlen_q * p.heads;
+  K.nlse.ss = 1;
+  K.nlse.sh = seq_rows;
+  K.nlse.sb = p.varlen ? 0 : (int64_t)p.heads * seq_rows;
 
   if (p.batch > 0 && (rows_q(p) > 0 || rows_k(p) > 0)) {
     if (fna2::launch_bwd_zero_uncovered(K, stream) != hipSuccess) return FNA2_E_LAUNCH;

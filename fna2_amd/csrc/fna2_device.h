@@ -20,6 +20,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 namespace fna2 {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -61,6 +64,17 @@ struct SeqExt {
   int q0, lq, k0, lk;
 };
 
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, unrolled at compile
+// time (for operands that must be immediates).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 // Marks a value that is the same in every lane as wave-uniform (scalar).
 __device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
@@ -81,14 +95,32 @@ __device__ __forceinline__ SeqExt seq_ext(const Problem& p, int b) {
   return e;
 }
 
+// Read-only data that a kernel reads at wave-uniform addresses is read
+// through the constant address space, so that the loads are scalar (s_load).
+// A vector load there would be followed by a vmcnt wait, which also waits for
+// every tile DMA in flight.
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(4))) T* const_space(const T* ptr) {
+  return (const __attribute__((address_space(4))) T*)ptr;
+}
+
 // Extents of a sequence b that is the same in every lane (scalar registers).
 __device__ __forceinline__ SeqExt seq_ext_uniform(const Problem& p, int b) {
-  const SeqExt e = seq_ext(p, b);
   SeqExt u;
-  u.q0 = uni(e.q0);
-  u.lq = uni(e.lq);
-  u.k0 = uni(e.k0);
-  u.lk = uni(e.lk);
+  if (p.varlen) {
+    const auto cq = const_space(p.cu_q);
+    const auto ck = const_space(p.cu_k);
+    b = uni(b);
+    int qs = cq[b], qe = cq[b + 1];
+    int ks = ck[b], ke = ck[b + 1];
+    qs = min(max(qs, 0), p.total_q);
+    qe = min(max(qe, qs), p.total_q);
+    ks = min(max(ks, 0), p.total_k);
+    ke = min(max(ke, ks), p.total_k);
+    u.q0 = qs; u.lq = qe - qs; u.k0 = ks; u.lk = ke - ks;
+  } else {
+    u.q0 = 0; u.lq = p.sq; u.k0 = 0; u.lk = p.sk;
+  }
   return u;
 }
 
@@ -100,13 +132,13 @@ struct __attribute__((aligned(32))) TileRec {
 
 __device__ __forceinline__ void tile_decode(const TileRec* __restrict__ tiles, int tix, int& b,
                                             int& t, SeqExt& e) {
-  const TileRec r = tiles[tix];
-  b = uni(r.b);
-  t = uni(r.t);
-  e.q0 = uni(r.q0);
-  e.lq = uni(r.lq);
-  e.k0 = uni(r.k0);
-  e.lk = uni(r.lk);
+  const auto r = const_space(tiles) + uni(tix);
+  b = uni(r->b);
+  t = uni(r->t);
+  e.q0 = uni(r->q0);
+  e.lq = uni(r->lq);
+  e.k0 = uni(r->k0);
+  e.lk = uni(r->lk);
 }
 
 // Base pointer of sequence b, head h of a view; row r is at base + r * ss.

@@ -52,7 +52,7 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
   int b, qt;
   SeqExt e;
   if (P.tiles) {
-    if (tix >= uni(*P.n_tiles)) return;
+    if (tix >= uni(*const_space(P.n_tiles))) return;
     tile_decode(P.tiles, tix, b, qt, e);
   } else {
     const int nqt = cdiv(p.sq, C::BM);

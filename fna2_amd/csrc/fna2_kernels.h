@@ -34,7 +34,7 @@ constexpr int kFwdBN = 64;
 // Backward: dK/dV kernel tiles keys by kKvBN and walks queries kKvBM at a
 // time; the dQ kernel tiles queries by kDqBM and walks keys kDqBN at a time.
 constexpr int kKvBN = 128;
-constexpr int kKvBM = 64;
+constexpr int kKvBM = 32;
 constexpr int kDqBM = 128;
 constexpr int kDqBN = 64;
 

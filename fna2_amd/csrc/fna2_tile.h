@@ -47,6 +47,57 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                            (int)kRsrcWord3);
 }
 
+// Buffer descriptor as four scalar words, for inline assembly.
+__device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t nbytes) {
+  const uint64_t a = (uint64_t)base;
+  u32x4 w;
+  w[0] = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  w[1] = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) & 0xffffu;
+  w[2] = __builtin_amdgcn_readfirstlane(nbytes);
+  w[3] = kRsrcWord3;
+  return w;
+}
+
+// LDS byte address of a pointer into shared memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Loads the compiler does not see as loads (inline assembly).  It therefore
+// inserts no wait for them, neither before a use of the destination nor
+// before an LDS read it cannot prove disjoint from an LDS DMA: every wait on
+// them is the caller's, explicit.
+//   dma_lds<16|4>: global -> LDS DMA of 16 (4) bytes per lane to lds + 16
+//     (4) * lane, from byte voffset of the buffer.
+//   load16_inplace<IMM>: 16 bytes at voffset + IMM into the registers that
+//     hold `dst` (which the caller must not read before its wait).
+// (The DMA takes its LDS address from M0, which it clobbers: nothing else
+// in these kernels keeps a value in M0.)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+template <int BYTES>
+__device__ __forceinline__ void dma_lds(const u32x4& rs, uint32_t lds, uint32_t voffset) {
+  static_assert(BYTES == 16 || BYTES == 4, "dword or dwordx4");
+  if constexpr (BYTES == 16)
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 1\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds), "v"(voffset), "s"(rs)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 1\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds), "v"(voffset), "s"(rs)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+template <int IMM>
+__device__ __forceinline__ void load16_inplace(u32x4& dst, const u32x4& rs, uint32_t voffset) {
+  static_assert(IMM >= 0 && IMM < 4096, "buffer offset field");
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3"
+               : "+v"(dst)
+               : "v"(voffset), "s"(rs), "i"(IMM));
+}
+
 // 2-bit chunk swizzle of a row (row bits 1..3).
 __device__ __forceinline__ int swz4(int r) {
   return ((((r >> 1) ^ (r >> 3)) & 1) << 1) | ((r >> 2) & 1);
@@ -100,6 +151,42 @@ struct Dma {
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rs, (lds_void*)(lds + i * 1024), 16, slot_offset(i, lane, row_bytes, valid_chunks), 0,
             0, 0);
+    }
+  }
+
+  // Issue exactly PER_WAVE instructions, whatever the wave: a share past
+  // the tile repeats share i % N (the same bytes to the same place, so the
+  // two writes agree).  The count of VMEM instructions is then a constant,
+  // which lets waits on the DMA ring be instruction immediates, and every
+  // destination lies in the tile (no select between LDS objects, which
+  // would defeat the compiler's alias analysis of DMA against LDS reads).
+  // Needs init_fixed.
+  __device__ __forceinline__ void init_fixed(int wave, int lane, uint32_t row_bytes,
+                                             int valid_chunks) {
+#pragma unroll
+    for (int j = 0; j < PER_WAVE; ++j)
+      voff[j] = slot_offset((wave + j * NWAVE) % N, lane, row_bytes, valid_chunks);
+  }
+  __device__ __forceinline__ void issue_fixed(const u32x4& rs, uint8_t* lds, int wave,
+                                              uint32_t add) const {
+#pragma unroll
+    for (int j = 0; j < PER_WAVE; ++j) {
+      const int i = (wave + j * NWAVE) % N;
+      dma_lds<16>(rs, lds_addr(lds + i * 1024), voff[j] + add);
+    }
+  }
+
+  // Issue this wave's share of a tile whose first row is `add` bytes past
+  // the descriptor's base (out-of-range lane offsets stay out of range as
+  // long as add < 2^31).
+  __device__ __forceinline__ void issue_at(__amdgpu_buffer_rsrc_t rs, uint8_t* lds, int wave,
+                                           uint32_t add) const {
+#pragma unroll
+    for (int j = 0; j < PER_WAVE; ++j) {
+      const int i = wave + j * NWAVE;
+      if (i < N)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(lds + i * 1024), 16,
+                                                 voff[j] + add, 0, 0, 0);
     }
   }
 

@@ -350,7 +350,8 @@ def _fna2_backward_varlen(
     cu_k = cu_seqlens_k.to(device=q.device, dtype=torch.int32).contiguous()
     gs = _gs32(graph_scale) if H_G else None
     lse = lse.contiguous()
-    delta = torch.empty(total_q, H, device=q.device, dtype=torch.float32)
+    # [T, H] view of head-major memory: the dK/dV kernel reads a head's rows
+    delta = torch.empty(H, total_q, device=q.device, dtype=torch.float32).t()
     dq, dk, dv, dr_q, dr_k = _grads_like(q, k, v, r_q, r_k, H_G)
     d_gs = torch.empty(max(H_G, 1), device=q.device, dtype=torch.float32)
     prob = _problem(True, N, max_seqlen_q, max_seqlen_k, total_q, total_k, H, H_KV, H_G, D, R,
