@@ -207,11 +207,6 @@ fna2::TView view(const fna2_tensor& t) {
   return v;
 }
 
-int max_iters(const fna2_problem& p, int hint, int total, int step) {
-  int64_t n = hint > 0 ? hint : total;
-  return (int)std::min<int64_t>(cdiv64(n, step), 1 << 20);
-}
-
 // Kernels exist for gfx950 only; cache the answer (and the CU count, which
 // sizes the persistent grids) per device.
 int check_device(int* num_cus = nullptr) {
@@ -344,10 +339,8 @@ int fna2_fwd(const fna2_fwd_args* a, void* stream_ptr) {
     const FwdWs w = fwd_ws(p);
     fna2::TileRec* tiles = (fna2::TileRec*)((char*)a->workspace + w.tiles);
     int* count = (int*)((char*)a->workspace + w.count);
-    fna2::TileSpec spec{0, kFwdBM, kFwdBN};
-    if (fna2::launch_build_tiles(K.p, spec, max_iters(p, p.seqlen_k, p.total_k, kFwdBN), tiles,
-                                 count, (int)g.fwd_bound, stream) != hipSuccess)
-      return FNA2_E_LAUNCH;
+    const fna2::TileList list{{0, kFwdBM, kFwdBN, 1}, tiles, count, (int)g.fwd_bound};
+    if (fna2::launch_build_tiles(K.p, list, nullptr, stream) != hipSuccess) return FNA2_E_LAUNCH;
     K.tiles = tiles;
     K.n_tiles = count;
   }
@@ -406,14 +399,9 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
       int* cq = (int*)((char*)a->workspace + w.count_q);
       fna2::TileRec* tk = (fna2::TileRec*)((char*)a->workspace + w.tiles_k);
       int* ck = (int*)((char*)a->workspace + w.count_k);
-      fna2::TileSpec sq{0, kDqBM, kDqBN};
-      fna2::TileSpec sk{1, kKvBN, kKvBM};
-      if (fna2::launch_build_tiles(K.p, sq, max_iters(p, p.seqlen_k, p.total_k, kDqBN), tq, cq,
-                                   (int)g.dq_bound, stream) != hipSuccess)
-        return FNA2_E_LAUNCH;
-      if (fna2::launch_build_tiles(K.p, sk, max_iters(p, p.seqlen_q, p.total_q, kKvBM), tk, ck,
-                                   (int)g.kv_bound, stream) != hipSuccess)
-        return FNA2_E_LAUNCH;
+      const fna2::TileList lq{{0, kDqBM, kDqBN, 1}, tq, cq, (int)g.dq_bound};
+      const fna2::TileList lk{{1, kKvBN, kKvBM, 0}, tk, ck, (int)g.kv_bound};
+      if (fna2::launch_build_tiles(K.p, lq, &lk, stream) != hipSuccess) return FNA2_E_LAUNCH;
       K.tiles_q = tq;
       K.n_tiles_q = cq;
       K.tiles_k = tk;

@@ -8,10 +8,15 @@ namespace fna2 {
 // kind 0: tiles of `tile` queries whose inner loop walks keys `step` at a time
 //         (forward, dQ).  kind 1: tiles of `tile` keys whose inner loop walks
 //         queries `step` at a time (dK/dV).
+// group: order sequences by total work and keep a sequence's tiles together
+// (tiles of one head that share K / V rows run together: L2 reuse); else
+// order every tile by its own work (the persistent dK/dV kernel, which deals
+// the list round-robin, balances better so).
 struct TileSpec {
   int kind;
   int tile;
   int step;
+  int group;
 };
 
 // Upper bound on the number of tiles for `extent` tokens in `nseq` sequences.
@@ -19,12 +24,17 @@ inline int64_t tile_bound(int64_t extent, int64_t nseq, int tile) {
   return (extent + tile - 1) / tile + nseq;
 }
 
-int tile_buckets(int max_iters);
+// One work list to build: its tile shape, output array (capacity `cap`)
+// and the device int that receives its length.
+struct TileList {
+  TileSpec spec;
+  TileRec* tiles;
+  int* count;
+  int cap;
+};
 
-// Builds `tiles` (TileRec: sequence, tile, extents) ordered by descending work and writes
-// the number of tiles to *count.  One workgroup.
-hipError_t launch_build_tiles(const Problem& p, const TileSpec& spec,
-                              int max_iters, TileRec* tiles, int* count, int cap,
+// Builds up to two lists in one launch (one workgroup each).
+hipError_t launch_build_tiles(const Problem& p, const TileList& a, const TileList* b,
                               hipStream_t stream);
 
 }  // namespace fna2

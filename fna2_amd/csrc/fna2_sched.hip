@@ -1,11 +1,17 @@
 // fna2_sched.hip — device-built work lists for the varlen kernels.
 //
-// A varlen launch has one workgroup per (tile, head).  The list of tiles is
-// built on the device from cu_seqlens (no host synchronisation) and ordered
-// longest-first by the number of inner-loop iterations, so that the
-// long-running tiles start first (LPT scheduling).  The reference instead
-// launches a (cdiv(max_seqlen, BLOCK), H, N) grid whose out-of-range
-// programs exit at once (FNA2/flash_naylis_attn.py:257-259, :784).
+// A varlen launch has one workgroup (or, for the persistent dK/dV kernel,
+// one work item) per (tile, head).  The list of tiles is built on the device
+// from cu_seqlens (no host synchronisation), longest-processing-time first
+// so that long work starts first.  Grouped lists order sequences by total
+// work and keep a sequence's tiles together, its longest tile first:
+// consecutive tiles of one head then run at about the same time and, with a
+// head count that is a multiple of 8 (tile-major grids with the head
+// fastest), on the same XCD, so the K / V rows they share come from HBM
+// once and from that XCD's L2 after.  Ungrouped lists order every tile by
+// its own work.  The reference instead launches a
+// (cdiv(max_seqlen, BLOCK), H, N) grid whose out-of-range programs exit at
+// once (FNA2/flash_naylis_attn.py:257-259, :784).
 #include "fna2_sched.h"
 
 namespace fna2 {
@@ -32,22 +38,42 @@ __device__ __forceinline__ int tile_work(const SeqExt& e, const TileSpec& s,
   return max(cdiv(e.lq, s.step) - lo, 0);
 }
 
-__global__ __launch_bounds__(kThreads) void build_tiles_kernel(
-    Problem p, TileSpec spec, int nbuckets, TileRec* __restrict__ tiles,
-    int* __restrict__ count, int cap) {
+__global__ __launch_bounds__(kThreads) void build_tiles_kernel(Problem p, TileList la,
+                                                               TileList lb) {
+  const TileList& L = blockIdx.x == 0 ? la : lb;
+  const TileSpec spec = L.spec;
+  TileRec* __restrict__ tiles = L.tiles;
+  int* __restrict__ count = L.count;
+  const int cap = L.cap;
+  constexpr int nbuckets = kMaxBuckets;
   __shared__ int hist[kMaxBuckets];
   __shared__ int warp_tot[kThreads / 64];
   const int tid = threadIdx.x;
   for (int i = tid; i < nbuckets; i += kThreads) hist[i] = 0;
   __syncthreads();
 
-  // Pass 1: histogram of work, bucket 0 = most work.
+  // Buckets: 0 = most work (work past the last bucket ties).  A grouped
+  // list buckets whole sequences by their total work, an ungrouped one
+  // buckets tiles by their own.  The histogram counts tiles, so its prefix
+  // sums are positions.
+  auto seq_bucket = [&](const SeqExt& e, int n) {
+    int w = 0;
+    for (int t = 0; t < n && w < nbuckets; ++t) w += tile_work(e, spec, p.causal, t);
+    return nbuckets - 1 - min(w, nbuckets - 1);
+  };
+  auto tile_bucket = [&](const SeqExt& e, int t) {
+    return nbuckets - 1 - min(tile_work(e, spec, p.causal, t), nbuckets - 1);
+  };
+
+  // Pass 1: tiles per bucket.
   for (int b = tid; b < p.nseq; b += kThreads) {
     const SeqExt e = seq_ext(p, b);
     const int n = tile_count(e, spec);
-    for (int t = 0; t < n; ++t) {
-      int w = min(tile_work(e, spec, p.causal, t), nbuckets - 1);
-      atomicAdd(&hist[nbuckets - 1 - w], 1);
+    if (n <= 0) continue;
+    if (spec.group) {
+      atomicAdd(&hist[seq_bucket(e, n)], n);
+    } else {
+      for (int t = 0; t < n; ++t) atomicAdd(&hist[tile_bucket(e, t)], 1);
     }
   }
   __syncthreads();
@@ -81,32 +107,36 @@ __global__ __launch_bounds__(kThreads) void build_tiles_kernel(
     *count = min(total, cap);
   }
 
-  // Pass 2: scatter (order inside a bucket is irrelevant: tiles are
-  // independent and each writes its own outputs).
+  // Pass 2: scatter (the order inside a bucket is irrelevant: tiles are
+  // independent and each writes its own outputs).  A grouped sequence
+  // claims a run of positions and writes its tiles most work first: under
+  // the causal mask the last query tile and the first key tile.
+  const bool reverse = spec.kind == 0 && p.causal;
   for (int b = tid; b < p.nseq; b += kThreads) {
     const SeqExt e = seq_ext(p, b);
     const int n = tile_count(e, spec);
-    for (int t = 0; t < n; ++t) {
-      int w = min(tile_work(e, spec, p.causal, t), nbuckets - 1);
-      int pos = atomicAdd(&hist[nbuckets - 1 - w], 1);
-      if (pos < cap) tiles[pos] = TileRec{b, t, e.q0, e.lq, e.k0, e.lk, 0, 0};
+    if (n <= 0) continue;
+    if (spec.group) {
+      const int pos = atomicAdd(&hist[seq_bucket(e, n)], n);
+      for (int i = 0; i < n; ++i) {
+        const int t = reverse ? n - 1 - i : i;
+        if (pos + i < cap) tiles[pos + i] = TileRec{b, t, e.q0, e.lq, e.k0, e.lk, 0, 0};
+      }
+    } else {
+      for (int t = 0; t < n; ++t) {
+        const int pos = atomicAdd(&hist[tile_bucket(e, t)], 1);
+        if (pos < cap) tiles[pos] = TileRec{b, t, e.q0, e.lq, e.k0, e.lk, 0, 0};
+      }
     }
   }
 }
 
 }  // namespace
 
-int tile_buckets(int max_iters) {
-  int nb = max_iters + 1;
-  if (nb < 1) nb = 1;
-  return nb > kMaxBuckets ? kMaxBuckets : nb;
-}
-
-hipError_t launch_build_tiles(const Problem& p, const TileSpec& spec,
-                              int max_iters, TileRec* tiles, int* count, int cap,
+hipError_t launch_build_tiles(const Problem& p, const TileList& a, const TileList* b,
                               hipStream_t stream) {
-  hipLaunchKernelGGL(build_tiles_kernel, dim3(1), dim3(kThreads), 0, stream, p,
-                     spec, tile_buckets(max_iters), tiles, count, cap);
+  hipLaunchKernelGGL(build_tiles_kernel, dim3(b ? 2 : 1), dim3(kThreads), 0, stream, p, a,
+                     b ? *b : a);
   return hipGetLastError();
 }
 
