@@ -11,8 +11,10 @@ Printed: ONE JSON line with the fwd+bwd throughput (``value``, TFLOP/s of
 algorithmic FLOPs: 4d+2r forward and 10d+6r backward per visible
 (query, key) pair per head), the forward-only throughput, fractions of the
 bf16 dense MFMA peak, a ``roofline`` object for the kernel that takes the
-most time per step (per-launch durations from HIP events recorded by the
-library on the launch stream during the timed steps), and a ``cpu_baseline``
+most time per step (per-launch durations from HIP events that the library
+records on its launch stream, in a second pass of the same steps: event
+records between dependent kernels add a few microseconds each, so the timed
+steps run without them), and a ``cpu_baseline``
 object: the reference's eager path (SDPA + materialised bias, restated in
 ``oracle/eager_reference.py``) timed on this host's cores on a bounded
 sample of the same workload.
@@ -324,17 +326,23 @@ def main():
         step()
     torch.cuda.synchronize()
 
-    # fwd+bwd, timed on the current stream with per-kernel events
-    timer = F.KernelTimer(args.steps, args.steps)
+    # fwd+bwd, timed on the current stream
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    with F.kernel_timing(timer):
-        e0.record()
-        for _ in range(args.steps):
-            step()
-        e1.record()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
     torch.cuda.synchronize()
     ms_step = e0.elapsed_time(e1) / args.steps
+
+    # per-kernel durations: the same steps again, with events around kernels
+    timer = F.KernelTimer(args.steps, args.steps)
+    torch.cuda.synchronize()
+    with F.kernel_timing(timer):
+        for _ in range(args.steps):
+            step()
+    torch.cuda.synchronize()
     kdur = {k: statistics.mean(v) for k, v in timer.durations_ms().items()}
 
     # forward only

@@ -543,6 +543,11 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       pipe_lds_mfma<2 * (2 * C::NDB + C::NRB), 2, 3>();
     };
 
+    // The last workgroup's consumers also reduce the dQ kernel's d_gs
+    // partials (complete: that kernel ran before this one), before their
+    // first block.
+    if (g == G - 1 && p.H_G > 0) reduce_dgs_waves(P, kw, C::NP, lane);
+
     KvCursor cc;  // the block being consumed
     start(cc, on_zero);
     // Step t consumes block t - 1 (nothing at t = 0).  The barrier does not

@@ -340,7 +340,8 @@ int fna2_fwd(const fna2_fwd_args* a, void* stream_ptr) {
     fna2::TileRec* tiles = (fna2::TileRec*)((char*)a->workspace + w.tiles);
     int* count = (int*)((char*)a->workspace + w.count);
     const fna2::TileList list{{0, kFwdBM, kFwdBN, 1}, tiles, count, (int)g.fwd_bound};
-    if (fna2::launch_build_tiles(K.p, list, nullptr, stream) != hipSuccess) return FNA2_E_LAUNCH;
+    if (fna2::launch_build_tiles(K.p, list, nullptr, nullptr, stream) != hipSuccess)
+      return FNA2_E_LAUNCH;
     K.tiles = tiles;
     K.n_tiles = count;
   }
@@ -379,6 +380,7 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
   const BwdWs w = bwd_ws(p);
   const Grids g = grids(p);
   K.dgs_partial = (float*)((char*)a->workspace + w.partial);
+  K.q_tiles = (int)g.q_tiles;
   const int rpl = fna2::padded_rank32(K.p.H_G, K.p.R);
   // Both are head-major (a head's rows are contiguous): the dK/dV kernel
   // reads them per head, 32 rows at a time.
@@ -393,7 +395,6 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
   K.nlse.sb = p.varlen ? 0 : (int64_t)p.heads * seq_rows;
 
   if (p.batch > 0 && (rows_q(p) > 0 || rows_k(p) > 0)) {
-    if (fna2::launch_bwd_zero_uncovered(K, stream) != hipSuccess) return FNA2_E_LAUNCH;
     if (p.varlen) {
       fna2::TileRec* tq = (fna2::TileRec*)((char*)a->workspace + w.tiles_q);
       int* cq = (int*)((char*)a->workspace + w.count_q);
@@ -401,7 +402,10 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
       int* ck = (int*)((char*)a->workspace + w.count_k);
       const fna2::TileList lq{{0, kDqBM, kDqBN, 1}, tq, cq, (int)g.dq_bound};
       const fna2::TileList lk{{1, kKvBN, kKvBM, 0}, tk, ck, (int)g.kv_bound};
-      if (fna2::launch_build_tiles(K.p, lq, &lk, stream) != hipSuccess) return FNA2_E_LAUNCH;
+      const fna2::ZeroRows zero{K.dq, K.drq, K.dk, K.dv, K.drk,
+                                (int)std::max(p.total_q, p.total_k)};
+      if (fna2::launch_build_tiles(K.p, lq, &lk, &zero, stream) != hipSuccess)
+        return FNA2_E_LAUNCH;
       K.tiles_q = tq;
       K.n_tiles_q = cq;
       K.tiles_k = tk;
@@ -418,7 +422,9 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
       return FNA2_E_LAUNCH;
     if (!mark(a->events, 3, stream)) return FNA2_E_LAUNCH;
   }
-  if (fna2::launch_bwd_dgs(K, (int)g.q_tiles, stream) != hipSuccess) return FNA2_E_LAUNCH;
+  // The dK/dV kernel reduces d_gs when it runs.
+  const bool dkdv_ran = p.batch > 0 && rows_k(p) > 0 && g.kv_grid > 0;
+  if (!dkdv_ran && fna2::launch_bwd_dgs(K, stream) != hipSuccess) return FNA2_E_LAUNCH;
   return FNA2_OK;
 }
 

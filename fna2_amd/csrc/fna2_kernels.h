@@ -22,6 +22,7 @@ struct BwdParams {
   const float* gs;
   float* dgs;            // [H_G]
   float* dgs_partial;    // [query tiles][4 waves][H_G] partial sums of d_gs
+  int q_tiles;           // query tiles of the dQ grid (varlen: capacity)
   const TileRec* tiles_q;  // varlen: query tiles (dQ kernel)
   const int* n_tiles_q;
   const TileRec* tiles_k;  // varlen: key tiles (dK/dV kernel)
@@ -45,9 +46,24 @@ inline int padded_rank32(int H_G, int R) {
 }
 
 hipError_t launch_fwd(const FwdParams& P, int rp, int grid, hipStream_t s);
-hipError_t launch_bwd_zero_uncovered(const BwdParams& P, hipStream_t s);
 hipError_t launch_bwd_dkdv(const BwdParams& P, int rpl, int grid, hipStream_t s);
 hipError_t launch_bwd_dq(const BwdParams& P, int rpl, int grid, hipStream_t s);
-hipError_t launch_bwd_dgs(const BwdParams& P, int q_tiles, hipStream_t s);
+hipError_t launch_bwd_dgs(const BwdParams& P, hipStream_t s);
+
+// d_gs[h] = sum of the dQ kernel's partials of head h in a fixed order
+// (deterministic), by one wave per head: wave w of `nw` takes heads w,
+// w + nw, ...  Shared by the reduce kernel and the dK/dV kernel, which does it
+// in passing when it runs.
+__device__ __forceinline__ void reduce_dgs_waves(const BwdParams& P, int w, int nw, int lane) {
+  const int tiles = P.n_tiles_q ? min(*P.n_tiles_q, P.q_tiles) : P.q_tiles;
+  const int rows = 4 * tiles, H_G = P.p.H_G;
+  for (int h = w; h < H_G; h += nw) {
+    float acc = 0.f;
+    for (int t = lane; t < rows; t += 64) acc += P.dgs_partial[(int64_t)t * H_G + h];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+    if (lane == 0) P.dgs[h] = acc;
+  }
+}
 
 }  // namespace fna2

@@ -33,8 +33,16 @@ struct TileList {
   int cap;
 };
 
-// Builds up to two lists in one launch (one workgroup each).
+// Gradient rows of tokens outside [cu[0], cu[N]) (varlen backward): no tile
+// covers them, so they are zeroed.  rows = 0: nothing to do.
+struct ZeroRows {
+  TView dq, drq, dk, dv, drk;
+  int rows;
+};
+
+// Builds up to two lists in one launch (one workgroup each); further
+// workgroups zero `zero`'s rows (1024 tokens each).
 hipError_t launch_build_tiles(const Problem& p, const TileList& a, const TileList* b,
-                              hipStream_t stream);
+                              const ZeroRows* zero, hipStream_t stream);
 
 }  // namespace fna2

@@ -38,8 +38,41 @@ __device__ __forceinline__ int tile_work(const SeqExt& e, const TileSpec& s,
   return max(cdiv(e.lq, s.step) - lo, 0);
 }
 
+// Zero the gradient rows of token t if it lies outside [cu[0], cu[N]).
+__device__ void zero_row(const Problem& p, const ZeroRows& z, int t) {
+  const int cq0 = p.cu_q[0], cqn = p.cu_q[p.nseq];
+  const int ck0 = p.cu_k[0], ckn = p.cu_k[p.nseq];
+  if (t < p.total_q && (t < cq0 || t >= cqn)) {
+    for (int h = 0; h < p.H; ++h) {
+      uint16_t* r = (uint16_t*)z.dq.ptr + (int64_t)t * z.dq.ss + (int64_t)h * z.dq.sh;
+      for (int d = 0; d < p.D; ++d) r[d] = 0;
+    }
+    for (int h = 0; h < p.H_G; ++h) {
+      uint16_t* r = (uint16_t*)z.drq.ptr + (int64_t)t * z.drq.ss + (int64_t)h * z.drq.sh;
+      for (int d = 0; d < p.R; ++d) r[d] = 0;
+    }
+  }
+  if (t < p.total_k && (t < ck0 || t >= ckn)) {
+    for (int h = 0; h < p.H_KV; ++h) {
+      uint16_t* r = (uint16_t*)z.dk.ptr + (int64_t)t * z.dk.ss + (int64_t)h * z.dk.sh;
+      uint16_t* s = (uint16_t*)z.dv.ptr + (int64_t)t * z.dv.ss + (int64_t)h * z.dv.sh;
+      for (int d = 0; d < p.D; ++d) r[d] = 0, s[d] = 0;
+    }
+    for (int h = 0; h < p.H_G; ++h) {
+      uint16_t* r = (uint16_t*)z.drk.ptr + (int64_t)t * z.drk.ss + (int64_t)h * z.drk.sh;
+      for (int d = 0; d < p.R; ++d) r[d] = 0;
+    }
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void build_tiles_kernel(Problem p, TileList la,
-                                                               TileList lb) {
+                                                               TileList lb, int nlists,
+                                                               ZeroRows zero) {
+  if ((int)blockIdx.x >= nlists) {
+    const int t = ((int)blockIdx.x - nlists) * kThreads + (int)threadIdx.x;
+    if (t < zero.rows) zero_row(p, zero, t);
+    return;
+  }
   const TileList& L = blockIdx.x == 0 ? la : lb;
   const TileSpec spec = L.spec;
   TileRec* __restrict__ tiles = L.tiles;
@@ -134,9 +167,13 @@ __global__ __launch_bounds__(kThreads) void build_tiles_kernel(Problem p, TileLi
 }  // namespace
 
 hipError_t launch_build_tiles(const Problem& p, const TileList& a, const TileList* b,
-                              hipStream_t stream) {
-  hipLaunchKernelGGL(build_tiles_kernel, dim3(b ? 2 : 1), dim3(kThreads), 0, stream, p, a,
-                     b ? *b : a);
+                              const ZeroRows* zero, hipStream_t stream) {
+  const int nlists = b ? 2 : 1;
+  ZeroRows z{};
+  if (zero) z = *zero;
+  const int zblocks = z.rows > 0 ? (z.rows + kThreads - 1) / kThreads : 0;
+  hipLaunchKernelGGL(build_tiles_kernel, dim3(nlists + zblocks), dim3(kThreads), 0, stream, p,
+                     a, b ? *b : a, nlists, z);
   return hipGetLastError();
 }
 

@@ -122,6 +122,32 @@ def test_varlen_empty_sequences(gpu):
     _varlen_case(gpu, [0, 40, 0, 0, 90, 0], 2, 64, 2, 2, 16, True, seed=15)
 
 
+def test_varlen_uncovered_rows(gpu):
+    """Tokens outside [cu[0], cu[N]) belong to no sequence: zero gradients there
+    (the launch that builds the tile lists also zeroes them), oracle parity
+    inside."""
+    F = _fna2()
+    lengths = [3, 40, 90, 5]
+    (q, k, v, rq, rk, gs_, dout, cu_q, cu_k) = H.make_varlen(lengths, 4, 64, 2, 3, 16, seed=21)
+    sub = cu_q[1:-1].clone()  # sequences 1 and 2 only: rows 0-2 and 133-137 uncovered
+    lo, hi = int(sub[0]), int(sub[-1])
+    scale = 0.125
+    print(f"varlen uncovered rows: cu {sub.tolist()} of {q.shape[0]} tokens", flush=True)
+    g = [t.to(gpu) for t in (q, k, v, rq, rk, gs_, dout, sub)]
+    out, lse = F._fna2_forward_varlen(g[0], g[1], g[2], g[3], g[4], g[5], g[7], g[7], 90, 90,
+                                      scale, True)
+    grads = F._fna2_backward_varlen(g[6], g[0], g[1], g[2], g[3], g[4], g[5], out, lse, g[7],
+                                    g[7], 90, 90, scale, True)
+    torch.cuda.synchronize()
+    ref_out, ref_lse, ref_g = H.oracle_fwd_bwd(q, k, v, rq, rk, gs_, dout, scale, True,
+                                               sub.numpy(), sub.numpy())
+    H.check_out(out[lo:hi], lse[lo:hi], np.asarray(ref_out)[lo:hi], np.asarray(ref_lse)[lo:hi])
+    for name, t in zip(("dq", "dk", "dv", "drq", "drk"), grads[:5]):
+        outside = torch.cat([t[:lo], t[hi:]]).float()
+        assert torch.count_nonzero(outside) == 0, f"{name}: nonzero gradient outside cu"
+    H.check_grads(grads, ref_g)
+
+
 def test_varlen_bias_dominated(gpu):
     # c5-like: rank 16 bias with R std 0.5 and non-causal attention
     _varlen_case(gpu, [300, 16, 128, 40, 77], 4, 64, 4, 4, 16, False, seed=16, gs=1.0,
