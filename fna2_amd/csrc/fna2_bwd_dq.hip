@@ -80,6 +80,32 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   const int wq_last = min(wq0 + 31, e.lq - 1);
   const int qrows = max(min(C::BM, e.lq - q0), 0);
 
+  int kv_hi = e.lk;
+  if (p.causal) kv_hi = min(kv_hi, min(e.lq, q0 + C::BM));
+  const int nkb = cdiv(max(kv_hi, 0), C::BN);
+
+  const uint32_t krb = (uint32_t)P.k.ss * 2u, vrb = (uint32_t)P.v.ss * 2u;
+  const uint32_t rkrb = (uint32_t)P.rk.ss * 2u;
+  Dma<C::BN, C::CD, C::NW> dk, dv;
+  Dma<C::BN, C::CR, C::NW> dr;
+  dk.init(wv, lane, krb, C::CD);
+  dv.init(wv, lane, vrb, C::CD);
+  if constexpr (RPL > 0) dr.init(wv, lane, rkrb, p.R / 8);
+  auto issue = [&](int it, uint8_t* st) {
+    const int k0 = it * C::BN;
+    const uint32_t rows = (uint32_t)max(min(C::BN, e.lk - k0), 0);
+    dk.issue(make_rsrc(kb + (int64_t)k0 * P.k.ss, rows * krb), st, wv);
+    if constexpr (RPL > 0) {
+      if (graph) dr.issue(make_rsrc(rkb + (int64_t)k0 * P.rk.ss, rows * rkrb), st + C::KB, wv);
+    }
+    dv.issue(make_rsrc(vb + (int64_t)k0 * P.v.ss, rows * vrb), st + C::KB + C::RB, wv);
+  };
+
+  // The first key tile's DMA goes out before the row loads below, so the
+  // two latencies overlap instead of adding up.
+  if (nkb > 0) issue(0, st0);
+  __builtin_amdgcn_sched_barrier(0);
+
   // Stationary B operands: Qa and dO rows of this lane's query.
   bf16x8 qreg[C::KSD + C::KSR];
   bf16x8 oreg[C::KSD];
@@ -151,27 +177,6 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
       }
     }
   }
-
-  int kv_hi = e.lk;
-  if (p.causal) kv_hi = min(kv_hi, min(e.lq, q0 + C::BM));
-  const int nkb = cdiv(max(kv_hi, 0), C::BN);
-
-  const uint32_t krb = (uint32_t)P.k.ss * 2u, vrb = (uint32_t)P.v.ss * 2u;
-  const uint32_t rkrb = (uint32_t)P.rk.ss * 2u;
-  Dma<C::BN, C::CD, C::NW> dk, dv;
-  Dma<C::BN, C::CR, C::NW> dr;
-  dk.init(wv, lane, krb, C::CD);
-  dv.init(wv, lane, vrb, C::CD);
-  if constexpr (RPL > 0) dr.init(wv, lane, rkrb, p.R / 8);
-  auto issue = [&](int it, uint8_t* st) {
-    const int k0 = it * C::BN;
-    const uint32_t rows = (uint32_t)max(min(C::BN, e.lk - k0), 0);
-    dk.issue(make_rsrc(kb + (int64_t)k0 * P.k.ss, rows * krb), st, wv);
-    if constexpr (RPL > 0) {
-      if (graph) dr.issue(make_rsrc(rkb + (int64_t)k0 * P.rk.ss, rows * rkrb), st + C::KB, wv);
-    }
-    dv.issue(make_rsrc(vb + (int64_t)k0 * P.v.ss, rows * vrb), st + C::KB + C::RB, wv);
-  };
 
   f32x16 acc[C::NDB + C::NRB];
 #pragma unroll
@@ -250,7 +255,6 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
       }
   };
 
-  if (nkb > 0) issue(0, st0);
   for (int it = 0; it < nkb; it += 2) {
     step(it, st0, st1);
     if (it + 1 < nkb) step(it + 1, st1, st0);

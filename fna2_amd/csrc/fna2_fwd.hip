@@ -76,6 +76,38 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
   const int wq_last = min(wq0 + 31, e.lq - 1);
   const int qrows = max(min(C::BM, e.lq - q0), 0);
 
+  int kv_hi = e.lk;
+  if (p.causal) kv_hi = min(kv_hi, min(e.lq, q0 + C::BM));
+  const int nkv = cdiv(max(kv_hi, 0), C::BN);
+
+  // DMA plans (lane offsets are tile-invariant; descriptors move per tile).
+  const uint32_t krb = (uint32_t)P.k.ss * 2u, vrb = (uint32_t)P.v.ss * 2u;
+  Dma<C::BN, C::CD, C::NW> dk, dv;
+  dk.init(wv, lane, krb, C::CD);
+  dv.init(wv, lane, vrb, C::CD);
+  Dma<C::BN, (C::CR > 0 ? C::CR : 4), C::NW> dr;
+  uint32_t rkrb = 0;
+  const uint16_t* rkb = kb;
+  if constexpr (C::CR > 0) {
+    rkrb = (uint32_t)P.rk.ss * 2u;
+    if (graph) rkb = seq_base<const uint16_t>(P.rk, p, b, e.k0, h);
+    dr.init(wv, lane, rkrb, p.R / 8);
+  }
+  auto issue = [&](int kt, uint8_t* base) {
+    const int k0 = kt * C::BN;
+    const uint32_t rows = (uint32_t)max(min(C::BN, e.lk - k0), 0);
+    dk.issue(make_rsrc(kb + (int64_t)k0 * P.k.ss, rows * krb), base, wv);
+    if constexpr (C::CR > 0) {
+      if (graph) dr.issue(make_rsrc(rkb + (int64_t)k0 * P.rk.ss, rows * rkrb), base + C::KBYTES, wv);
+    }
+    dv.issue(make_rsrc(vb + (int64_t)k0 * P.v.ss, rows * vrb), base + C::KBYTES + C::RBYTES, wv);
+  };
+
+  // The first key tile's DMA goes out before the query loads below, so the
+  // two latencies overlap instead of adding up.
+  if (nkv > 0) issue(0, stage0);
+  __builtin_amdgcn_sched_barrier(0);
+
   // Query operand (B of S^T): lane holds Qa[qrow][16s + 8hl .. +7].
   bf16x8 qreg[C::KSD + C::KSR];
   {
@@ -104,33 +136,6 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
       }
     }
   }
-
-  int kv_hi = e.lk;
-  if (p.causal) kv_hi = min(kv_hi, min(e.lq, q0 + C::BM));
-  const int nkv = cdiv(max(kv_hi, 0), C::BN);
-
-  // DMA plans (lane offsets are tile-invariant; descriptors move per tile).
-  const uint32_t krb = (uint32_t)P.k.ss * 2u, vrb = (uint32_t)P.v.ss * 2u;
-  Dma<C::BN, C::CD, C::NW> dk, dv;
-  dk.init(wv, lane, krb, C::CD);
-  dv.init(wv, lane, vrb, C::CD);
-  Dma<C::BN, (C::CR > 0 ? C::CR : 4), C::NW> dr;
-  uint32_t rkrb = 0;
-  const uint16_t* rkb = kb;
-  if constexpr (C::CR > 0) {
-    rkrb = (uint32_t)P.rk.ss * 2u;
-    if (graph) rkb = seq_base<const uint16_t>(P.rk, p, b, e.k0, h);
-    dr.init(wv, lane, rkrb, p.R / 8);
-  }
-  auto issue = [&](int kt, uint8_t* base) {
-    const int k0 = kt * C::BN;
-    const uint32_t rows = (uint32_t)max(min(C::BN, e.lk - k0), 0);
-    dk.issue(make_rsrc(kb + (int64_t)k0 * P.k.ss, rows * krb), base, wv);
-    if constexpr (C::CR > 0) {
-      if (graph) dr.issue(make_rsrc(rkb + (int64_t)k0 * P.rk.ss, rows * rkrb), base + C::KBYTES, wv);
-    }
-    dv.issue(make_rsrc(vb + (int64_t)k0 * P.v.ss, rows * vrb), base + C::KBYTES + C::RBYTES, wv);
-  };
 
   f32x16 oacc[D / 32];
 #pragma unroll
@@ -214,7 +219,6 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
         oacc[d] = mfma32(tr_operand<C::BN>(vl, tl, 16 * s, 32 * d), pb[s], oacc[d]);
   };
 
-  if (nkv > 0) issue(0, stage0);
   for (int kt = 0; kt < nkv; kt += 2) {
     step(kt, stage0, stage1);
     if (kt + 1 < nkv) step(kt + 1, stage1, stage0);
