@@ -66,7 +66,10 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // Loads the compiler does not see as loads (inline assembly).  It therefore
 // inserts no wait for them, neither before a use of the destination nor
 // before an LDS read it cannot prove disjoint from an LDS DMA: every wait on
-// them is the caller's, explicit.
+// them is the caller's, explicit.  Nor does its hazard recognizer see the
+// buffer instruction: a VALU write of an SGPR (v_readfirstlane of a
+// descriptor word) needs 5 wait states before a VMEM instruction reads it,
+// so each block starts with s_nop 4.
 //   dma_lds<16|4>: global -> LDS DMA of 16 (4) bytes per lane to lds + 16
 //     (4) * lane, from byte voffset of the buffer.
 //   load16_inplace<IMM>: 16 bytes at voffset + IMM into the registers that
@@ -79,12 +82,12 @@ template <int BYTES>
 __device__ __forceinline__ void dma_lds(const u32x4& rs, uint32_t lds, uint32_t voffset) {
   static_assert(BYTES == 16 || BYTES == 4, "dword or dwordx4");
   if constexpr (BYTES == 16)
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 1\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                  :
                  : "s"(lds), "v"(voffset), "s"(rs)
                  : "memory", "m0");
   else
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 1\n\tbuffer_load_dword %1, %2, 0 offen lds"
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dword %1, %2, 0 offen lds"
                  :
                  : "s"(lds), "v"(voffset), "s"(rs)
                  : "memory", "m0");
@@ -93,7 +96,7 @@ __device__ __forceinline__ void dma_lds(const u32x4& rs, uint32_t lds, uint32_t 
 template <int IMM>
 __device__ __forceinline__ void load16_inplace(u32x4& dst, const u32x4& rs, uint32_t voffset) {
   static_assert(IMM >= 0 && IMM < 4096, "buffer offset field");
-  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3"
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3"
                : "+v"(dst)
                : "v"(voffset), "s"(rs), "i"(IMM));
 }

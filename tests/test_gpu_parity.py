@@ -111,6 +111,14 @@ def test_varlen_mixed(gpu, causal):
     _varlen_case(gpu, lengths, 4, 64, 4, 4, 16, causal, seed=12)
 
 
+def test_varlen_d64_rank_rows_past_20k(gpu):
+    """d 64, 8 graph heads of rank 32: a tile's rank rows past 20 KB.  Caught a
+    missing wait state between a scalar descriptor write and the inline-asm
+    buffer load that reads it."""
+    _varlen_case(gpu, [37, 128, 5, 90], 8, 64, 8, 8, 32, True, seed=22)
+    _varlen_case(gpu, [300], 8, 64, 8, 8, 32, False, seed=23)
+
+
 def test_varlen_cross_lengths(gpu):
     lq = [50, 130, 7, 200]
     lk = [70, 100, 7, 260]
