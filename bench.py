@@ -19,7 +19,12 @@ object: the reference's eager path (SDPA + materialised bias, restated in
 ``oracle/eager_reference.py``) timed on this host's cores on a bounded
 sample of the same workload.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3]
+``--rope`` measures the varlen rotary embedding kernel instead (q and k of
+the c3 pack: 16384 tokens, 16 + 16 heads, d = 128, bf16): its HBM rate and
+roofline fraction, the reference's per-sequence eager loop on the same GPU,
+and the oracle on the host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3] [--rope]
 """
 from __future__ import annotations
 
@@ -44,6 +49,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c3", choices=["c2", "c3", "c4", "c5"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--rope", action="store_true",
+                    help="measure the varlen RoPE kernel (c3 pack) instead of attention")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU-baseline budget (seconds)")
     ap.add_argument("--no-flush", action="store_true",
@@ -277,8 +284,104 @@ def cpu_baseline(cfg, inp, budget_s):
     }
 
 
+def rope_bench(args):
+    """Varlen RoPE of q [T, 16, 128] and k [T, 16, 128] (bf16, the c3 pack)."""
+    import numpy as np
+    import torch
+
+    from fna2_amd import _capi, attention_fna2, configs
+    from fna2_amd.rope import rope_varlen_raw
+
+    _capi.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = configs.get("c3")
+    lengths = cfg.seq_lengths()
+    cu_list = [0] + list(np.cumsum(lengths))
+    T, H, D = cu_list[-1], 16, 128
+    g = torch.Generator().manual_seed(42)
+    q = torch.randn(T, H, D, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(T, H, D, generator=g).to(torch.bfloat16).to(dev)
+    cu = torch.tensor(cu_list, dtype=torch.int32, device=dev)
+    rope = attention_fna2.RotaryPositionalEmbedding(D, max_seq_len=1024).to(dev)
+    inv = rope.inv_freq
+
+    for _ in range(args.warmup):
+        rope_varlen_raw(q, k, cu, inv)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        rope_varlen_raw(q, k, cu, inv)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    nbytes = 2 * (q.numel() + k.numel()) * q.element_size() + cu.numel() * 4 + inv.numel() * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+
+    # the reference's algorithm on the same GPU: a host loop over the sequences
+    # (cu_seqlens.tolist()) applying the dense RoPE (attention_fna2.py:620-647)
+    def eager():
+        qo, ko = torch.empty_like(q), torch.empty_like(k)
+        off = 0
+        for n in (cu[1:] - cu[:-1]).tolist():
+            qs = q[off:off + n].transpose(0, 1).unsqueeze(0)
+            ks = k[off:off + n].transpose(0, 1).unsqueeze(0)
+            qr, kr = rope(qs, ks, position_offset=0)
+            qo[off:off + n] = qr.squeeze(0).transpose(0, 1)
+            ko[off:off + n] = kr.squeeze(0).transpose(0, 1)
+            off += n
+        return qo, ko
+    for _ in range(3):
+        eager()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(10):
+        eager()
+    torch.cuda.synchronize()
+    ms_eager = (time.perf_counter() - t0) / 10 * 1e3
+
+    line = {
+        "metric": "varlen RoPE HBM GB/s (q and k read + written once)",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k)",
+        "config": {"workload": f"rope_varlen: c3 pack, {T} tokens / {len(lengths)} seqs, "
+                               f"q and k {H} heads each, d={D}"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "rope_kernel", "algorithmic_bytes": nbytes},
+        "eager_reference_ms": round(ms_eager, 3),
+        "speedup_over_eager": round(ms_eager / ms, 1),
+    }
+    if not args.no_cpu:
+        from oracle import rope_oracle as RO
+        n = 2048  # leading tokens of the pack
+        qc = q[:n].float().cpu().numpy()
+        kc = k[:n].float().cpu().numpy()
+        cuc = [c for c in cu_list if c <= n] + ([n] if cu_list[-1] > n else [])
+        RO.rope_varlen(qc, kc, cuc, inv.cpu().numpy(), "bf16")
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            RO.rope_varlen(qc, kc, cuc, inv.cpu().numpy(), "bf16")
+            ts.append(time.perf_counter() - t0)
+        med = statistics.median(ts)
+        line["cpu_baseline"] = {"value": round(nbytes * n / T / med / 1e9, 3), "unit": "GB/s",
+                                "cores": 1, "kind": "port",
+                                "sample": f"oracle (numpy) on the first {n} of {T} tokens, "
+                                          f"median of 3: {med * 1e3:.1f} ms"}
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
+    if args.rope:
+        rope_bench(args)
+        return
     if args.copy_calibration:
         copy_calibration()
         return

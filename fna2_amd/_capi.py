@@ -17,6 +17,8 @@ from pathlib import Path
 LIB_PATH = Path(os.environ.get("FNA2_LIB", Path(__file__).resolve().parent / "libfna2_hip.so"))
 
 FNA2_BF16 = 1
+FNA2_F16 = 2
+FNA2_F32 = 3
 
 STATUS = {
     0: "FNA2_OK",
@@ -32,10 +34,11 @@ STATUS = {
     -10: "FNA2_E_LAUNCH",
     -11: "FNA2_E_DEVICE",
     -12: "FNA2_E_SCALE",
+    -13: "FNA2_E_ALIAS",
 }
 # Contract violations surface as AssertionError, like the reference's asserts
 # (FNA2/flash_naylis_attn.py:718-720, :778, :1419-1427); the rest as RuntimeError.
-_ASSERT_CODES = {-1, -2, -3, -4, -5, -6, -7, -8, -12}
+_ASSERT_CODES = {-1, -2, -3, -4, -5, -6, -7, -8, -12, -13}
 
 
 class Tensor(ctypes.Structure):
@@ -114,6 +117,24 @@ class BwdArgs(ctypes.Structure):
     ]
 
 
+class RopeArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("total_tokens", ctypes.c_int32),
+        ("heads_q", ctypes.c_int32),
+        ("heads_k", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("nseq", ctypes.c_int32),
+        ("sign", ctypes.c_int32),
+        ("cu_seqlens", ctypes.c_void_p),
+        ("inv_freq", ctypes.c_void_p),
+        ("q", Tensor),
+        ("k", Tensor),
+        ("q_out", Tensor),
+        ("k_out", Tensor),
+    ]
+
+
 # Every symbol the header declares, with its ctypes signature.
 SIGNATURES = {
     "fna2_version": (ctypes.c_int, []),
@@ -124,6 +145,8 @@ SIGNATURES = {
     "fna2_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Problem)]),
     "fna2_fwd": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.c_void_p]),
     "fna2_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), ctypes.c_void_p]),
+    "fna2_check_rope": (ctypes.c_int, [ctypes.POINTER(RopeArgs)]),
+    "fna2_rope_varlen": (ctypes.c_int, [ctypes.POINTER(RopeArgs), ctypes.c_void_p]),
 }
 
 _lib = None

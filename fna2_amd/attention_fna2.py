@@ -21,8 +21,9 @@ multiple of 8 up to 64 rather than only ``BLOCK_R`` (:225-229).  The FNA2 op
 itself never falls back: called without the library it raises.
 
 Varlen RoPE restarts positions at every sequence, as the reference's
-``_apply_rope_varlen`` (:620-647), with the positions formed on the device
-(no per-call host synchronisation).
+``_apply_rope_varlen`` (:620-647), in one launch of the HIP rotary kernel
+(``fna2_amd.rope``) with the positions formed on the device (no per-call
+host synchronisation).
 """
 from __future__ import annotations
 
@@ -35,6 +36,7 @@ import torch.nn.functional as F
 
 from . import _capi
 from .flash_naylis_attn import BLOCK_R, flash_naylis_attn, rank_supported
+from .rope import rope_varlen
 
 
 def _detect_fna2() -> bool:
@@ -83,7 +85,7 @@ class RotaryPositionalEmbedding(nn.Module):
         self.yarn_scale = yarn_scale
         self.yarn_original_max_len = yarn_original_max_len
         half = torch.arange(0, dim, 2, dtype=torch.float32)
-        inv_freq = base ** (-half / dim)
+        inv_freq = 1.0 / (base ** (half / dim))  # as attention_fna2.py:121-122
         if use_yarn and yarn_scale != 1.0:
             # frequencies past the first max(dim/2, dim/4) even indices are
             # divided by a factor rising linearly from 1 to yarn_scale
@@ -121,16 +123,9 @@ class RotaryPositionalEmbedding(nn.Module):
 
     def forward_varlen(self, q: torch.Tensor, k: torch.Tensor,
                        cu_seqlens: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
-        """q [T, H, D], k [T, H_KV, D]; position of token t = t - cu[seq(t)]."""
-        T = q.shape[0]
-        cu = cu_seqlens.to(device=q.device, dtype=torch.long)
-        t = torch.arange(T, device=q.device)
-        seq = torch.searchsorted(cu, t, right=True) - 1
-        pos = (t - cu[seq.clamp(min=0)]).clamp(min=0)
-        ang = torch.outer(pos.to(q.dtype), self.inv_freq.to(device=q.device, dtype=q.dtype))
-        ang = torch.cat((ang, ang), dim=-1)[:, None, :]
-        cos, sin = ang.cos(), ang.sin()
-        return self.rotate(q, cos, sin), self.rotate(k, cos, sin)
+        """q [T, H, D], k [T, H_KV, D]; position of token t = t - cu[seq(t)]
+        (the HIP rotary kernel; GPU tensors only)."""
+        return rope_varlen(q, k, cu_seqlens, self.inv_freq)
 
 
 class NaylisAttention(nn.Module):

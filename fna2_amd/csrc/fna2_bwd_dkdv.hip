@@ -34,11 +34,11 @@
 // Q, bf16(b Rq), dO, -LSE log2(e) and delta tiles stream in by DMA (issued by
 // the producers) through a four-stage ring that runs two blocks ahead of the
 // producers, across item boundaries; the consumers read a stage one block
-// later.  At the first block of an (item, head) the producers start loading
-// the rows of the next one into a second register set.  Both roles meet at
-// one barrier per block.  The stages are separate LDS objects and the loops
-// are unrolled by four so that the compiler can prove that reads and
-// in-flight DMA never alias.
+// later.  The last block of an (item, head) loads the rows of the next one
+// into the registers its MFMAs have just read.  Both roles meet at one
+// barrier per block.  The stages are separate LDS objects and the loops are
+// unrolled by four so that the compiler can prove that reads and in-flight
+// DMA never alias.
 #include "fna2_kernels.h"
 #include "fna2_tile.h"
 

@@ -237,7 +237,7 @@ const char* fna2_status_string(int s) {
   switch (s) {
     case FNA2_OK: return "ok";
     case FNA2_E_NULL: return "a required pointer is NULL";
-    case FNA2_E_DTYPE: return "unsupported dtype (bf16 only)";
+    case FNA2_E_DTYPE: return "unsupported dtype (attention: bf16 only)";
     case FNA2_E_HEAD_DIM: return "head_dim must be 64 or 128";
     case FNA2_E_RANK: return "rank must be a multiple of 8 in [8, 64]";
     case FNA2_E_HEADS: return "heads must be a multiple of heads_kv and heads_graph <= heads";
@@ -248,6 +248,7 @@ const char* fna2_status_string(int s) {
     case FNA2_E_LAUNCH: return "kernel launch failed";
     case FNA2_E_DEVICE: return "current device is not gfx950";
     case FNA2_E_SCALE: return "softmax_scale must be finite";
+    case FNA2_E_ALIAS: return "an output overlaps its input without being equal to it";
   }
   return "unknown status";
 }
@@ -425,6 +426,91 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
   // The dK/dV kernel reduces d_gs when it runs.
   const bool dkdv_ran = p.batch > 0 && rows_k(p) > 0 && g.kv_grid > 0;
   if (!dkdv_ran && fna2::launch_bwd_dgs(K, stream) != hipSuccess) return FNA2_E_LAUNCH;
+  return FNA2_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Byte range [lo, hi) a [T, heads, D] view covers.
+void rope_extent(const fna2_tensor& t, int T, int heads, int D, size_t es, uintptr_t& lo,
+                 uintptr_t& hi) {
+  int64_t a = 0, b = D;
+  const int64_t ds = (int64_t)(T - 1) * t.stride_s, dh = (int64_t)(heads - 1) * t.stride_h;
+  (ds < 0 ? a : b) += ds;
+  (dh < 0 ? a : b) += dh;
+  lo = (uintptr_t)t.ptr + (uintptr_t)(a * (int64_t)es);
+  hi = (uintptr_t)t.ptr + (uintptr_t)(b * (int64_t)es);
+}
+
+int rope_pair(const fna2_tensor& in, const fna2_tensor& out, int T, int heads, int D,
+              size_t es) {
+  if (!in.ptr || !out.ptr) return FNA2_E_NULL;
+  for (const fna2_tensor* t : {&in, &out}) {
+    if ((uintptr_t)t->ptr % 16 || (t->stride_s * (int64_t)es) % 16 ||
+        (t->stride_h * (int64_t)es) % 16)
+      return FNA2_E_STRIDE;
+  }
+  if (in.ptr == out.ptr)
+    return in.stride_s == out.stride_s && in.stride_h == out.stride_h ? FNA2_OK : FNA2_E_ALIAS;
+  uintptr_t l0, h0, l1, h1;
+  rope_extent(in, T, heads, D, es, l0, h0);
+  rope_extent(out, T, heads, D, es, l1, h1);
+  return (l0 < h1 && l1 < h0) ? FNA2_E_ALIAS : FNA2_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fna2_check_rope(const fna2_rope_args* a) {
+  if (!a) return FNA2_E_NULL;
+  if (a->dtype != FNA2_BF16 && a->dtype != FNA2_F16 && a->dtype != FNA2_F32) return FNA2_E_DTYPE;
+  const int D = a->head_dim;
+  if (D < 16 || D > 512 || (D & (D - 1)) != 0) return FNA2_E_HEAD_DIM;
+  if (a->total_tokens < 0 || a->heads_q < 0 || a->heads_k < 0 || a->nseq < 0 ||
+      (a->sign != 1 && a->sign != -1))
+    return FNA2_E_SHAPE;
+  if (a->total_tokens == 0 || a->heads_q + a->heads_k == 0) return FNA2_OK;
+  if (!a->cu_seqlens) return FNA2_E_SEQLENS;
+  if (!a->inv_freq) return FNA2_E_NULL;
+  const size_t es = a->dtype == FNA2_F32 ? 4 : 2;
+  if (a->heads_q > 0) FNA2_TRY(rope_pair(a->q, a->q_out, a->total_tokens, a->heads_q, D, es));
+  if (a->heads_k > 0) FNA2_TRY(rope_pair(a->k, a->k_out, a->total_tokens, a->heads_k, D, es));
+  return FNA2_OK;
+}
+
+int fna2_rope_varlen(const fna2_rope_args* a, void* stream) {
+  FNA2_TRY(fna2_check_rope(a));
+  if (a->total_tokens == 0 || a->heads_q + a->heads_k == 0) return FNA2_OK;
+  FNA2_TRY(check_device());
+  fna2::RopeParams P;
+  std::memset(&P, 0, sizeof(P));
+  P.dtype = a->dtype == FNA2_BF16 ? fna2::kRopeBF16
+            : a->dtype == FNA2_F16 ? fna2::kRopeF16
+                                   : fna2::kRopeF32;
+  P.T = a->total_tokens;
+  P.Hq = a->heads_q;
+  P.Hk = a->heads_k;
+  P.D = a->head_dim;
+  P.nseq = a->nseq;
+  P.sign = a->sign;
+  P.cu = a->cu_seqlens;
+  P.inv_freq = a->inv_freq;
+  P.q = a->q.ptr;
+  P.k = a->k.ptr;
+  P.q_out = a->q_out.ptr;
+  P.k_out = a->k_out.ptr;
+  P.q_ss = a->q.stride_s;
+  P.q_sh = a->q.stride_h;
+  P.k_ss = a->k.stride_s;
+  P.k_sh = a->k.stride_h;
+  P.qo_ss = a->q_out.stride_s;
+  P.qo_sh = a->q_out.stride_h;
+  P.ko_ss = a->k_out.stride_s;
+  P.ko_sh = a->k_out.stride_h;
+  if (fna2::launch_rope(P, (hipStream_t)stream) != hipSuccess) return FNA2_E_LAUNCH;
   return FNA2_OK;
 }
 

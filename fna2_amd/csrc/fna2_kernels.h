@@ -17,8 +17,8 @@ struct BwdParams {
   Problem p;
   TView q, k, v, rq, rk, o, lse, dout, delta, dq, dk, dv, drq, drk;
   // Workspace written by the dQ kernel for the dK/dV kernel:
-  TView rqs;   // bf16(b_h Rq), [rows][H_G][rank width]
-  TView nlse;  // -LSE log2(e), fp32 [rows][H]
+  TView rqs;   // bf16(b_h Rq), [H_G][rows][rank width]
+  TView nlse;  // -LSE log2(e), fp32 [H][rows]
   const float* gs;
   float* dgs;            // [H_G]
   float* dgs_partial;    // [query tiles][4 waves][H_G] partial sums of d_gs
@@ -44,6 +44,21 @@ constexpr int kDqBN = 64;
 inline int padded_rank32(int H_G, int R) {
   return (H_G > 0 && R > 0) ? ((R + 31) / 32) * 32 : 0;
 }
+
+// Varlen rotary embedding (fna2_rope.hip).  Element strides; q_out/k_out
+// equal q/k (in place) or are disjoint from them.
+constexpr int kRopeBF16 = 1, kRopeF16 = 2, kRopeF32 = 3;
+struct RopeParams {
+  int dtype, T, Hq, Hk, D, nseq, sign;
+  const int* cu;         // [nseq + 1]
+  const float* inv_freq;  // [D / 2]
+  const void* q;
+  const void* k;
+  void* q_out;
+  void* k_out;
+  int64_t q_ss, q_sh, k_ss, k_sh, qo_ss, qo_sh, ko_ss, ko_sh;
+};
+hipError_t launch_rope(const RopeParams& P, hipStream_t s);
 
 hipError_t launch_fwd(const FwdParams& P, int rp, int grid, hipStream_t s);
 hipError_t launch_bwd_dkdv(const BwdParams& P, int rpl, int grid, hipStream_t s);

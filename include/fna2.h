@@ -38,8 +38,9 @@ extern "C" {
 
 #define FNA2_ABI_VERSION 1
 
-/* Element type of q, k, v, r_q, r_k, out, dout and of the gradients. */
-enum fna2_dtype { FNA2_BF16 = 1 };
+/* Element types.  The attention entry points take FNA2_BF16 (q, k, v, r_q,
+ * r_k, out, dout and the gradients); fna2_rope_varlen takes all three. */
+enum fna2_dtype { FNA2_BF16 = 1, FNA2_F16 = 2, FNA2_F32 = 3 };
 
 /* Return codes. */
 enum fna2_status {
@@ -55,7 +56,8 @@ enum fna2_status {
   FNA2_E_WORKSPACE = -9,   /* workspace missing or too small                 */
   FNA2_E_LAUNCH = -10,     /* a kernel launch failed                         */
   FNA2_E_DEVICE = -11,     /* current device is not gfx950                   */
-  FNA2_E_SCALE = -12       /* softmax_scale not finite                       */
+  FNA2_E_SCALE = -12,      /* softmax_scale not finite                       */
+  FNA2_E_ALIAS = -13       /* an output overlaps its input without equal it  */
 };
 
 /* A bf16/fp32 tensor view: base pointer + element strides. */
@@ -128,6 +130,40 @@ typedef struct fna2_bwd_args {
    * and the dK/dV/dRk kernel. */
   void* const* events;
 } fna2_bwd_args;
+
+/* Varlen rotary position embedding: positions restart at 0 in every packed
+ * sequence.  For token t of sequence b (cu_seqlens[b] <= t < cu_seqlens[b+1]),
+ * p = t - cu_seqlens[b], and i < D/2:
+ *     angle_i   = p * inv_freq[i]
+ *     y_i       = x_i cos(angle_i) - x_{i+D/2} sin(angle_i)
+ *     y_{i+D/2} = x_{i+D/2} cos(angle_i) + x_i sin(angle_i)
+ * for every head of q and of k, each step rounded to the element type where
+ * the reference's eager code rounds (position, inv_freq, angle, cos, sin,
+ * each product, the sum).  sign = -1 rotates by -angle_i (the gradient:
+ * dx from dy).  Tokens outside [cu_seqlens[0], cu_seqlens[N]) are copied
+ * unchanged.  Replaces NaylisAttention._apply_rope_varlen with
+ * RotaryPositionalEmbedding.forward (FNA2/attention_fna2.py:620-647,
+ * :143-170), which loops over the sequences on the host. */
+typedef struct fna2_rope_args {
+  int32_t dtype;        /* enum fna2_dtype: q, k, q_out, k_out             */
+  int32_t total_tokens; /* T                                               */
+  int32_t heads_q;      /* heads of q (0: q absent)                        */
+  int32_t heads_k;      /* heads of k (0: k absent)                        */
+  int32_t head_dim;     /* D: a power of two in [16, 512]                  */
+  int32_t nseq;         /* N >= 0                                          */
+  int32_t sign;         /* +1 rotate, -1 rotate back                       */
+  const int32_t* cu_seqlens; /* [N+1] device int32, nondecreasing          */
+  const float* inv_freq;     /* [D/2] device fp32                           */
+  fna2_tensor q, k;          /* [T, heads, D] (stride_s, stride_h)         */
+  fna2_tensor q_out, k_out;  /* written; each equal to its input or disjoint */
+} fna2_rope_args;
+
+/* Host-only validation of a rotary call (shapes, strides, alignment,
+ * aliasing); no GPU call. */
+int fna2_check_rope(const fna2_rope_args* args);
+
+/* Rotary embedding of q and k on the stream given (one launch). */
+int fna2_rope_varlen(const fna2_rope_args* args, void* hip_stream);
 
 /* ABI version (FNA2_ABI_VERSION). */
 int fna2_version(void);

@@ -1,8 +1,8 @@
 """NaylisAttention drop-in (fna2_amd/attention_fna2.py).
 
 CPU: the constructor / forward signatures of the reference
-(FNA2/attention_fna2.py:197-215, :380-390), the device-side varlen RoPE
-against per-sequence RoPE, and the eager (non-FNA2) path.
+(FNA2/attention_fna2.py:197-215, :380-390) and the eager (non-FNA2) path.
+(The varlen RoPE kernel has its own tests: tests/test_rope.py.)
 GPU: the FNA2 path (HIP kernels) against the module's eager SDPA path with the
 same weights, dense (GQA + vanilla heads) and packed varlen against the dense
 path run per sequence.
@@ -34,24 +34,6 @@ def test_signatures_match_reference():
     assert _params(A.NaylisAttention.__init__) == CTOR
     assert _params(A.NaylisAttention.forward) == FWD
     assert A._FNA2_BLOCK_R == 32
-
-
-def test_varlen_rope_equals_per_sequence_rope():
-    torch.manual_seed(0)
-    rope = A.RotaryPositionalEmbedding(64, max_seq_len=512)
-    lens = [5, 17, 1, 40]
-    cu = torch.tensor([0, 5, 22, 23, 63], dtype=torch.int32)
-    q = torch.randn(sum(lens), 4, 64)
-    k = torch.randn(sum(lens), 2, 64)
-    qo, ko = rope.forward_varlen(q, k, cu)
-    off = 0
-    for n in lens:
-        qs = q[off:off + n].transpose(0, 1)[None]
-        ks = k[off:off + n].transpose(0, 1)[None]
-        qr, kr = rope(qs, ks)
-        torch.testing.assert_close(qo[off:off + n], qr[0].transpose(0, 1), atol=1e-5, rtol=1e-5)
-        torch.testing.assert_close(ko[off:off + n], kr[0].transpose(0, 1), atol=1e-5, rtol=1e-5)
-        off += n
 
 
 def test_yarn_scale_and_frequencies():
