@@ -5,15 +5,20 @@
 //
 // One workgroup = 4 waves = 128 queries of one (sequence, head); wave w owns
 // queries 32w..32w+31 and keeps its augmented query operand [a Q | b Rq]
-// in registers.  Per 64-key step the wave computes the transposed score tile
-// S^T = Ka Qa^T (64 keys x 32 queries) with one MFMA chain over the
-// augmented width D + R (the bias is fused into the same contraction), so
+// in registers.  Per key step (64 keys at d = 64, 32 at d = 128) the wave
+// computes the transposed score tile S^T = Ka Qa^T (keys x 32 queries) with
+// one MFMA chain over the augmented width D + R (the bias is fused into the
+// same contraction), so
 // each lane holds one query column and the row softmax needs one exchange
 // (lane ^ 32).  The bf16 probabilities are the B operand of
 // O^T += V^T P^T straight from the accumulator registers; V^T comes from
 // the row-major V tile through ds_read_b64_tr_b16.  K, Rk and V tiles are
 // DMA'd global -> LDS (buffer_load ... lds, zero-filled past the sequence)
 // into a two-stage ring: the next tile streams in while this one computes.
+// At d = 128 the 32-key step keeps a wave within 168 registers and a
+// workgroup within 40 KB of LDS, so three workgroups share a CU and cover
+// each other's row-load and DMA latency (two at 64 keys); at d = 64 the
+// 64-key step already leaves room for more.
 #include "fna2_kernels.h"
 #include "fna2_tile.h"
 
@@ -25,7 +30,7 @@ template <int D, int RPL>
 struct FwdCfg {
   static constexpr int NW = 4;
   static constexpr int BM = kFwdBM;
-  static constexpr int BN = kFwdBN;
+  static constexpr int BN = D == 128 ? 32 : kFwdBN;  // keys per step
   static constexpr int CD = D / 8;      // chunks per K / V row
   static constexpr int CR = RPL / 8;    // chunks per Rk row (0 without graph heads)
   static constexpr int KSD = D / 16;    // 16-deep steps over the head dim
@@ -247,17 +252,17 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
 }
 
 // One non-template kernel per (D, padded rank): every kernel gets its own
-// host launch stub.
-#define FNA2_FWD_KERNEL(D, RPL)                                                       \
-  __global__ __launch_bounds__(256, 2) void fwd_kernel_d##D##_r##RPL(const FwdParams P) { \
-    fwd_body<D, RPL>(P);                                                              \
+// host launch stub.  WAVES: waves per SIMD the register budget is cut for.
+#define FNA2_FWD_KERNEL(D, RPL, WAVES)                                                     \
+  __global__ __launch_bounds__(256, WAVES) void fwd_kernel_d##D##_r##RPL(const FwdParams P) { \
+    fwd_body<D, RPL>(P);                                                                   \
   }
-FNA2_FWD_KERNEL(64, 0)
-FNA2_FWD_KERNEL(64, 32)
-FNA2_FWD_KERNEL(64, 64)
-FNA2_FWD_KERNEL(128, 0)
-FNA2_FWD_KERNEL(128, 32)
-FNA2_FWD_KERNEL(128, 64)
+FNA2_FWD_KERNEL(64, 0, 2)
+FNA2_FWD_KERNEL(64, 32, 2)
+FNA2_FWD_KERNEL(64, 64, 2)
+FNA2_FWD_KERNEL(128, 0, 3)
+FNA2_FWD_KERNEL(128, 32, 3)
+FNA2_FWD_KERNEL(128, 64, 3)
 #undef FNA2_FWD_KERNEL
 
 }  // namespace
