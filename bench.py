@@ -24,7 +24,11 @@ the c3 pack: 16384 tokens, 16 + 16 heads, d = 128, bf16): its HBM rate and
 roofline fraction, the reference's per-sequence eager loop on the same GPU,
 and the oracle on the host.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3] [--rope]
+``--producer`` measures the projection that produces the kernels' operands
+(q, k, v, R_q, R_k from x: one GEMM over the stacked weights, forward and
+backward) against the reference's five separate projections.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3] [--rope|--producer]
 """
 from __future__ import annotations
 
@@ -51,6 +55,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--rope", action="store_true",
                     help="measure the varlen RoPE kernel (c3 pack) instead of attention")
+    ap.add_argument("--producer", action="store_true",
+                    help="measure the fused operand projection (c3-sized module) instead")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU-baseline budget (seconds)")
     ap.add_argument("--no-flush", action="store_true",
@@ -377,8 +383,73 @@ def rope_bench(args):
     print(json.dumps(line), flush=True)
 
 
+def producer_bench(args):
+    """q, k, v, R_q, R_k of a c3-sized NaylisAttention (T = 16384, E = 2048,
+    16 heads of 128, 16 graph heads of rank 32, bf16), forward + backward."""
+    import torch
+
+    from fna2_amd import attention_fna2 as A
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    T, E = 16384, 2048
+    torch.manual_seed(0)
+    m = A.NaylisAttention(E, 16, rel_rank=32, use_fna2=False).to(dev).to(torch.bfloat16)
+    x = torch.randn(T, E, device=dev, dtype=torch.bfloat16, requires_grad=True)
+    params = [m.q_proj.weight, m.k_proj.weight, m.v_proj.weight, m.rel_q_proj.weight,
+              m.rel_k_proj.weight]
+    H, D, HG, R = 16, 128, 16, 32
+    grads = [torch.randn(T, H, D, device=dev, dtype=torch.bfloat16) for _ in range(3)] + \
+            [torch.randn(T, HG, R, device=dev, dtype=torch.bfloat16) for _ in range(2)]
+
+    def separate():  # attention_fna2.py:554-556, :326-334
+        q = m.q_proj(x).view(T, H, D)
+        k = m.k_proj(x).view(T, H, D)
+        v = m.v_proj(x).view(T, H, D)
+        rq = m.rel_q_proj(x).view(T, HG, R).to(torch.bfloat16).contiguous()
+        rk = m.rel_k_proj(x).view(T, HG, R).to(torch.bfloat16).contiguous()
+        return q, k, v, rq, rk
+
+    def run(fn):
+        outs = fn()
+        torch.autograd.grad(outs, [x] + params, grads)
+
+    res = {}
+    for name, fn in (("separate", separate), ("fused", lambda: m._project(x))):
+        for _ in range(args.warmup):
+            run(fn)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            run(fn)
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = e0.elapsed_time(e1) / args.steps
+    n_all = E + 2 * H * D + 2 * HG * R
+    flops = 3 * 2 * T * E * n_all  # forward GEMM, dX and dW GEMMs
+    tf = flops / (res["fused"] * 1e-3) / 1e12
+    print(json.dumps({
+        "metric": "operand producer fwd+bwd TFLOP/s (one GEMM over stacked q/k/v/R weights)",
+        "value": round(tf, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(res["fused"], 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) x and upstream gradients)",
+        "config": {"workload": f"producer: T={T}, E={E}, q/k/v 16x128, R_q/R_k 16x32"},
+        "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None, "kernel": "hipBLASLt GEMMs"},
+        "separate_ms": round(res["separate"], 4),
+        "speedup_over_separate": round(res["separate"] / res["fused"], 3),
+        "cpu_baseline": None,
+    }), flush=True)
+
+
 def main():
     args = parse()
+    if args.producer:
+        producer_bench(args)
+        return
     if args.rope:
         rope_bench(args)
         return

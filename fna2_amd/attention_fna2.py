@@ -209,14 +209,34 @@ class NaylisAttention(nn.Module):
             return math.sqrt(self.rope.yarn_scale) / math.sqrt(self.head_dim)
         return 1.0 / math.sqrt(self.head_dim)
 
-    def _rel(self, x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
-        """R_q, R_k in bf16: [B, H_G, S, R] from [B, S, E], or [T, H_G, R] from [T, E]."""
-        shape = x.shape[:-1] + (self.graph_heads, self.rel_rank)
-        r_q = self.rel_q_proj(x).view(shape).to(torch.bfloat16)
-        r_k = self.rel_k_proj(x).view(shape).to(torch.bfloat16)
-        if x.dim() == 3:
-            r_q, r_k = r_q.transpose(1, 2), r_k.transpose(1, 2)
-        return r_q.contiguous(), r_k.contiguous()
+    def _project(self, x: torch.Tensor):
+        """q, k, v and (with graph heads) R_q, R_k from ONE GEMM over the
+        stacked weights [W_q; W_k; W_v; W_rq; W_rk]: views into its
+        [.., E + 2 kv_dim + 2 H_G R] output, which the HIP kernels read
+        through their strides.  Replaces the five projections of
+        attention_fna2.py:401-403, :554-556 and _compute_rq_rk(_varlen)
+        (:301-335): x is read once, and R needs no .contiguous() copy.  The
+        parameters stay separate (state dicts unchanged)."""
+        ws = [self.q_proj.weight, self.k_proj.weight, self.v_proj.weight]
+        if self.graph_heads > 0:
+            ws += [self.rel_q_proj.weight, self.rel_k_proj.weight]
+        y = F.linear(x, torch.cat(ws, dim=0))
+        gr = self.graph_heads * self.rel_rank
+        sizes = [self.embed_dim, self.kv_dim, self.kv_dim] + ([gr, gr] if gr else [])
+        parts = list(torch.split(y, sizes, dim=-1))
+        lead = x.shape[:-1]
+        q = parts[0].view(lead + (self.num_heads, self.head_dim))
+        k = parts[1].view(lead + (self.n_kv_heads, self.head_dim))
+        v = parts[2].view(lead + (self.n_kv_heads, self.head_dim))
+        r_q = r_k = None
+        if gr:
+            r_q = parts[3].view(lead + (self.graph_heads, self.rel_rank)).to(torch.bfloat16)
+            r_k = parts[4].view(lead + (self.graph_heads, self.rel_rank)).to(torch.bfloat16)
+        if x.dim() == 3:  # [B, S, h, *] -> [B, h, S, *]
+            q, k, v = (t.transpose(1, 2) for t in (q, k, v))
+            if gr:
+                r_q, r_k = r_q.transpose(1, 2), r_k.transpose(1, 2)
+        return q, k, v, r_q, r_k
 
     def _dense_bias(self, x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
         """gs_h R_q R_k^T for graph heads (zeros for vanilla heads), [B, H, S, S]."""
@@ -257,9 +277,14 @@ class NaylisAttention(nn.Module):
                                         max_seqlen_k)
         B, S, _ = x.shape
         scale = self._attn_scale()
-        q = self.q_proj(x).view(B, S, self.num_heads, self.head_dim).transpose(1, 2)
-        k = self.k_proj(x).view(B, S, self.n_kv_heads, self.head_dim).transpose(1, 2)
-        v = self.v_proj(x).view(B, S, self.n_kv_heads, self.head_dim).transpose(1, 2)
+        fused = (self._use_fna2 and self.graph_heads > 0 and self.soft_cap is None
+                 and past_kv is None)
+        if fused:
+            q, k, v, r_q, r_k = self._project(x)
+        else:
+            q = self.q_proj(x).view(B, S, self.num_heads, self.head_dim).transpose(1, 2)
+            k = self.k_proj(x).view(B, S, self.n_kv_heads, self.head_dim).transpose(1, 2)
+            v = self.v_proj(x).view(B, S, self.n_kv_heads, self.head_dim).transpose(1, 2)
         if self.use_qk_norm:
             q, k = self.q_norm(q), self.k_norm(k)
         offset = past_kv[0].shape[2] if past_kv is not None else 0
@@ -276,8 +301,7 @@ class NaylisAttention(nn.Module):
         is_causal = S > 1 and past_kv is None
         use_graph = self.graph_heads > 0 and (S > 1 or past_kv is None)
 
-        if self._use_fna2 and use_graph and self.soft_cap is None and past_kv is None:
-            r_q, r_k = self._rel(x)
+        if fused:
             out = _flash_naylis_attn(q, k, v, r_q, r_k, self.graph_scale.to(torch.float32),
                                      softmax_scale=scale, is_causal=is_causal)
         else:
@@ -320,9 +344,7 @@ class NaylisAttention(nn.Module):
         """x [T, E] packed (attention_fna2.py:533-617); causal within each sequence."""
         T = x.shape[0]
         scale = self._attn_scale()
-        q = self.q_proj(x).view(T, self.num_heads, self.head_dim)
-        k = self.k_proj(x).view(T, self.n_kv_heads, self.head_dim)
-        v = self.v_proj(x).view(T, self.n_kv_heads, self.head_dim)
+        q, k, v, r_q, r_k = self._project(x)
         if self.use_qk_norm:
             q, k = self.q_norm(q), self.k_norm(k)
         if self.rope is not None:
@@ -336,11 +358,7 @@ class NaylisAttention(nn.Module):
         if not self._use_fna2:
             raise RuntimeError("varlen NaylisAttention needs the FNA2 HIP kernels "
                                "(gfx950 and libfna2_hip.so)")
-        if self.graph_heads > 0:
-            r_q, r_k = self._rel(x)
-            gs = self.graph_scale.to(torch.float32)
-        else:
-            r_q = r_k = gs = None
+        gs = self.graph_scale.to(torch.float32) if self.graph_heads > 0 else None
         out = _flash_naylis_attn(q, k, v, r_q, r_k, gs, softmax_scale=scale, is_causal=True,
                                  cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_k,
                                  max_seqlen_q=msq, max_seqlen_k=msk)

@@ -113,3 +113,26 @@ def test_fna2_varlen_matches_dense_per_sequence(gpu):
         yd, _ = fast(x[off:off + n][None])
         assert (y[off:off + n] - yd[0]).abs().max().item() < 2e-2
         off += n
+
+
+@pytest.mark.parametrize("lead", [(37,), (2, 19)])
+def test_fused_projection_equals_separate_projections(lead):
+    """One GEMM over the stacked weights gives the five projections
+    (attention_fna2.py:401-403, :301-335) as views of one output."""
+    torch.manual_seed(1)
+    m = A.NaylisAttention(128, 8, n_kv_heads=2, rel_rank=16, vanilla_heads=2, use_fna2=False)
+    x = torch.randn(*lead, 128)
+    q, k, v, rq, rk = m._project(x)
+    H, D, HKV, HG, R = 8, 16, 2, 6, 16
+    sep = [m.q_proj(x).view(*lead, H, D), m.k_proj(x).view(*lead, HKV, D),
+           m.v_proj(x).view(*lead, HKV, D), m.rel_q_proj(x).view(*lead, HG, R),
+           m.rel_k_proj(x).view(*lead, HG, R)]
+    if len(lead) == 2:
+        sep = [t.transpose(1, 2) for t in sep]
+    for got, want in zip((q, k, v), sep[:3]):
+        torch.testing.assert_close(got, want, atol=1e-5, rtol=1e-5)
+    for got, want in zip((rq, rk), sep[3:]):
+        assert got.dtype == torch.bfloat16
+        torch.testing.assert_close(got.float(), want.to(torch.bfloat16).float(), atol=1e-2, rtol=0)
+    # q, k, v are views of one buffer (no copies)
+    assert q.untyped_storage().data_ptr() == k.untyped_storage().data_ptr() == v.untyped_storage().data_ptr()
