@@ -296,7 +296,7 @@ def rope_bench(args):
     import torch
 
     from fna2_amd import _capi, attention_fna2, configs
-    from fna2_amd.rope import rope_varlen_raw
+    from fna2_amd.rope import rope_varlen, rope_varlen_raw
 
     _capi.lib()
     dev = torch.device("cuda:0")
@@ -347,6 +347,49 @@ def rope_bench(args):
     torch.cuda.synchronize()
     ms_eager = (time.perf_counter() - t0) / 10 * 1e3
 
+    # QK-RMSNorm + RoPE in one launch, forward + backward (fp32 norm weights),
+    # against the eager chain the reference runs (q_norm / k_norm then the
+    # per-sequence RoPE, attention_fna2.py:558-566)
+    wq = torch.ones(D, device=dev, requires_grad=True)
+    wk = torch.ones(D, device=dev, requires_grad=True)
+    qg, kg = q.detach().requires_grad_(True), k.detach().requires_grad_(True)
+    gq, gk = torch.randn_like(q), torch.randn_like(k)
+
+    def timed(fn, n):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n
+
+    def norm_fwd():
+        return rope_varlen(qg, kg, cu, inv, wq, wk, 1e-6)
+
+    def norm_fwd_bwd():
+        yq, yk = norm_fwd()
+        torch.autograd.grad([yq, yk], [qg, kg, wq, wk], [gq, gk])
+    ms_norm_fwd = timed(lambda: rope_varlen_raw(q, k, cu, inv, 1, wq, wk, 1e-6), args.steps)
+    ms_norm_fb = timed(norm_fwd_bwd, args.steps)
+    qn, kn = attention_fna2.RMSNorm(D).to(dev), attention_fna2.RMSNorm(D).to(dev)
+
+    def eager_norm_fwd_bwd():
+        a, b = qn(qg), kn(kg)
+        qo, ko = torch.empty_like(a), torch.empty_like(b)
+        off = 0
+        for n in (cu[1:] - cu[:-1]).tolist():
+            qr, kr = rope(a[off:off + n].transpose(0, 1).unsqueeze(0),
+                          b[off:off + n].transpose(0, 1).unsqueeze(0))
+            qo[off:off + n] = qr.squeeze(0).transpose(0, 1)
+            ko[off:off + n] = kr.squeeze(0).transpose(0, 1)
+            off += n
+        torch.autograd.grad([qo, ko], [qg, kg, qn.weight, kn.weight], [gq, gk])
+    ms_eager_norm_fb = timed(eager_norm_fwd_bwd, 5)
+
     line = {
         "metric": "varlen RoPE HBM GB/s (q and k read + written once)",
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -360,6 +403,13 @@ def rope_bench(args):
                      "kernel": "rope_kernel", "algorithmic_bytes": nbytes},
         "eager_reference_ms": round(ms_eager, 3),
         "speedup_over_eager": round(ms_eager / ms, 1),
+        "qk_norm_rope": {
+            "fwd_ms": round(ms_norm_fwd, 4),
+            "fwd_GBps": round(nbytes / (ms_norm_fwd * 1e-3) / 1e9, 1),
+            "fwd_bwd_ms": round(ms_norm_fb, 4),
+            "eager_fwd_bwd_ms": round(ms_eager_norm_fb, 3),
+            "speedup_over_eager": round(ms_eager_norm_fb / ms_norm_fb, 1),
+        },
     }
     if not args.no_cpu:
         from oracle import rope_oracle as RO

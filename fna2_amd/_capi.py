@@ -132,6 +132,23 @@ class RopeArgs(ctypes.Structure):
         ("k", Tensor),
         ("q_out", Tensor),
         ("k_out", Tensor),
+        ("norm_q", ctypes.c_void_p),
+        ("norm_k", ctypes.c_void_p),
+        ("norm_eps", ctypes.c_float),
+    ]
+
+
+class RopeBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("fwd", RopeArgs),
+        ("dq_out", Tensor),
+        ("dk_out", Tensor),
+        ("dq", Tensor),
+        ("dk", Tensor),
+        ("dnorm_q", ctypes.c_void_p),
+        ("dnorm_k", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -147,6 +164,9 @@ SIGNATURES = {
     "fna2_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), ctypes.c_void_p]),
     "fna2_check_rope": (ctypes.c_int, [ctypes.POINTER(RopeArgs)]),
     "fna2_rope_varlen": (ctypes.c_int, [ctypes.POINTER(RopeArgs), ctypes.c_void_p]),
+    "fna2_rope_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(RopeArgs)]),
+    "fna2_check_rope_bwd": (ctypes.c_int, [ctypes.POINTER(RopeBwdArgs)]),
+    "fna2_rope_bwd": (ctypes.c_int, [ctypes.POINTER(RopeBwdArgs), ctypes.c_void_p]),
 }
 
 _lib = None

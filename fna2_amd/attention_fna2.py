@@ -121,11 +121,14 @@ class RotaryPositionalEmbedding(nn.Module):
         sin = sin[position_offset:position_offset + s][None, None]
         return self.rotate(q, cos, sin), self.rotate(k, cos, sin)
 
-    def forward_varlen(self, q: torch.Tensor, k: torch.Tensor,
-                       cu_seqlens: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    def forward_varlen(self, q: torch.Tensor, k: torch.Tensor, cu_seqlens: torch.Tensor,
+                       norm_q: Optional[torch.Tensor] = None,
+                       norm_k: Optional[torch.Tensor] = None,
+                       eps: float = 1e-6) -> Tuple[torch.Tensor, torch.Tensor]:
         """q [T, H, D], k [T, H_KV, D]; position of token t = t - cu[seq(t)]
-        (the HIP rotary kernel; GPU tensors only)."""
-        return rope_varlen(q, k, cu_seqlens, self.inv_freq)
+        (the HIP rotary kernel; GPU tensors only).  With norm weights the
+        rows are RMS-normalised first, in the same launch."""
+        return rope_varlen(q, k, cu_seqlens, self.inv_freq, norm_q, norm_k, eps)
 
 
 class NaylisAttention(nn.Module):
@@ -345,10 +348,15 @@ class NaylisAttention(nn.Module):
         T = x.shape[0]
         scale = self._attn_scale()
         q, k, v, r_q, r_k = self._project(x)
-        if self.use_qk_norm:
+        if self.rope is not None:  # QK-RMSNorm (if any) and RoPE in one launch
+            assert not self.use_qk_norm or self.q_norm.eps == self.k_norm.eps
+            q, k = self.rope.forward_varlen(
+                q, k, cu_seqlens_q,
+                self.q_norm.weight if self.use_qk_norm else None,
+                self.k_norm.weight if self.use_qk_norm else None,
+                self.q_norm.eps if self.use_qk_norm else 1e-6)
+        elif self.use_qk_norm:
             q, k = self.q_norm(q), self.k_norm(k)
-        if self.rope is not None:
-            q, k = self.rope.forward_varlen(q, k, cu_seqlens_q)
         orig_dtype = q.dtype
         if q.dtype == torch.float32:
             q, k, v = (t.to(torch.bfloat16) for t in (q, k, v))

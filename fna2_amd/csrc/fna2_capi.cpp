@@ -460,11 +460,8 @@ int rope_pair(const fna2_tensor& in, const fna2_tensor& out, int T, int heads, i
   return (l0 < h1 && l1 < h0) ? FNA2_E_ALIAS : FNA2_OK;
 }
 
-}  // namespace
-
-extern "C" {
-
-int fna2_check_rope(const fna2_rope_args* a) {
+// Checks shared by the forward and the backward (no tensors).
+int rope_common(const fna2_rope_args* a) {
   if (!a) return FNA2_E_NULL;
   if (a->dtype != FNA2_BF16 && a->dtype != FNA2_F16 && a->dtype != FNA2_F32) return FNA2_E_DTYPE;
   const int D = a->head_dim;
@@ -472,19 +469,21 @@ int fna2_check_rope(const fna2_rope_args* a) {
   if (a->total_tokens < 0 || a->heads_q < 0 || a->heads_k < 0 || a->nseq < 0 ||
       (a->sign != 1 && a->sign != -1))
     return FNA2_E_SHAPE;
+  if ((a->norm_q || a->norm_k) && !(std::isfinite(a->norm_eps) && a->norm_eps >= 0.f))
+    return FNA2_E_SCALE;
   if (a->total_tokens == 0 || a->heads_q + a->heads_k == 0) return FNA2_OK;
   if (!a->cu_seqlens) return FNA2_E_SEQLENS;
   if (!a->inv_freq) return FNA2_E_NULL;
-  const size_t es = a->dtype == FNA2_F32 ? 4 : 2;
-  if (a->heads_q > 0) FNA2_TRY(rope_pair(a->q, a->q_out, a->total_tokens, a->heads_q, D, es));
-  if (a->heads_k > 0) FNA2_TRY(rope_pair(a->k, a->k_out, a->total_tokens, a->heads_k, D, es));
   return FNA2_OK;
 }
 
-int fna2_rope_varlen(const fna2_rope_args* a, void* stream) {
-  FNA2_TRY(fna2_check_rope(a));
-  if (a->total_tokens == 0 || a->heads_q + a->heads_k == 0) return FNA2_OK;
-  FNA2_TRY(check_device());
+bool rope_empty(const fna2_rope_args* a) {
+  return a->total_tokens == 0 || a->heads_q + a->heads_k == 0;
+}
+
+size_t rope_esize(const fna2_rope_args* a) { return a->dtype == FNA2_F32 ? 4 : 2; }
+
+fna2::RopeParams rope_params(const fna2_rope_args* a) {
   fna2::RopeParams P;
   std::memset(&P, 0, sizeof(P));
   P.dtype = a->dtype == FNA2_BF16 ? fna2::kRopeBF16
@@ -500,17 +499,111 @@ int fna2_rope_varlen(const fna2_rope_args* a, void* stream) {
   P.inv_freq = a->inv_freq;
   P.q = a->q.ptr;
   P.k = a->k.ptr;
-  P.q_out = a->q_out.ptr;
-  P.k_out = a->k_out.ptr;
   P.q_ss = a->q.stride_s;
   P.q_sh = a->q.stride_h;
   P.k_ss = a->k.stride_s;
   P.k_sh = a->k.stride_h;
-  P.qo_ss = a->q_out.stride_s;
-  P.qo_sh = a->q_out.stride_h;
-  P.ko_ss = a->k_out.stride_s;
-  P.ko_sh = a->k_out.stride_h;
+  P.wq = a->heads_q > 0 ? a->norm_q : nullptr;
+  P.wk = a->heads_k > 0 ? a->norm_k : nullptr;
+  P.eps = a->norm_eps;
+  return P;
+}
+
+void rope_out(fna2::RopeParams& P, const fna2_tensor& qo, const fna2_tensor& ko) {
+  P.q_out = qo.ptr;
+  P.k_out = ko.ptr;
+  P.qo_ss = qo.stride_s;
+  P.qo_sh = qo.stride_h;
+  P.ko_ss = ko.stride_s;
+  P.ko_sh = ko.stride_h;
+}
+
+size_t rope_ws(const fna2_rope_args* a) {
+  if (!(a->norm_q || a->norm_k) || rope_empty(a)) return 0;
+  return align_up(sizeof(float) * 2u * (size_t)fna2::rope_blocks(a->total_tokens) *
+                  (size_t)a->head_dim);
+}
+
+}  // namespace
+
+extern "C" {
+
+int fna2_check_rope(const fna2_rope_args* a) {
+  FNA2_TRY(rope_common(a));
+  if (rope_empty(a)) return FNA2_OK;
+  const int T = a->total_tokens, D = a->head_dim;
+  const size_t es = rope_esize(a);
+  if (a->heads_q > 0) FNA2_TRY(rope_pair(a->q, a->q_out, T, a->heads_q, D, es));
+  if (a->heads_k > 0) FNA2_TRY(rope_pair(a->k, a->k_out, T, a->heads_k, D, es));
+  return FNA2_OK;
+}
+
+int fna2_rope_varlen(const fna2_rope_args* a, void* stream) {
+  FNA2_TRY(fna2_check_rope(a));
+  if (rope_empty(a)) return FNA2_OK;
+  FNA2_TRY(check_device());
+  fna2::RopeParams P = rope_params(a);
+  rope_out(P, a->q_out, a->k_out);
   if (fna2::launch_rope(P, (hipStream_t)stream) != hipSuccess) return FNA2_E_LAUNCH;
+  return FNA2_OK;
+}
+
+size_t fna2_rope_bwd_workspace_bytes(const fna2_rope_args* a) {
+  if (!a || rope_common(a) != FNA2_OK) return 0;
+  return rope_ws(a);
+}
+
+int fna2_check_rope_bwd(const fna2_rope_bwd_args* b) {
+  if (!b) return FNA2_E_NULL;
+  const fna2_rope_args* a = &b->fwd;
+  FNA2_TRY(rope_common(a));
+  if (rope_empty(a)) return FNA2_OK;
+  const int T = a->total_tokens, D = a->head_dim;
+  const size_t es = rope_esize(a);
+  const bool norm = a->norm_q || a->norm_k;
+  if (a->heads_q > 0) {
+    FNA2_TRY(rope_pair(b->dq_out, b->dq, T, a->heads_q, D, es));
+    if (norm) FNA2_TRY(rope_pair(a->q, b->dq, T, a->heads_q, D, es));
+    if (a->norm_q && !b->dnorm_q) return FNA2_E_NULL;
+  }
+  if (a->heads_k > 0) {
+    FNA2_TRY(rope_pair(b->dk_out, b->dk, T, a->heads_k, D, es));
+    if (norm) FNA2_TRY(rope_pair(a->k, b->dk, T, a->heads_k, D, es));
+    if (a->norm_k && !b->dnorm_k) return FNA2_E_NULL;
+  }
+  const size_t need = rope_ws(a);
+  if (need && (!b->workspace || b->workspace_bytes < need)) return FNA2_E_WORKSPACE;
+  return FNA2_OK;
+}
+
+int fna2_rope_bwd(const fna2_rope_bwd_args* b, void* stream) {
+  FNA2_TRY(fna2_check_rope_bwd(b));
+  const fna2_rope_args* a = &b->fwd;
+  if (rope_empty(a)) return FNA2_OK;
+  FNA2_TRY(check_device());
+  fna2::RopeParams P = rope_params(a);
+  rope_out(P, b->dq, b->dk);
+  if (!(P.wq || P.wk)) {  // the inverse rotation of the gradients
+    P.q = b->dq_out.ptr;
+    P.k = b->dk_out.ptr;
+    P.q_ss = b->dq_out.stride_s;
+    P.q_sh = b->dq_out.stride_h;
+    P.k_ss = b->dk_out.stride_s;
+    P.k_sh = b->dk_out.stride_h;
+    P.sign = -a->sign;
+    if (fna2::launch_rope(P, (hipStream_t)stream) != hipSuccess) return FNA2_E_LAUNCH;
+    return FNA2_OK;
+  }
+  P.gq = b->dq_out.ptr;
+  P.gk = b->dk_out.ptr;
+  P.gq_ss = b->dq_out.stride_s;
+  P.gq_sh = b->dq_out.stride_h;
+  P.gk_ss = b->dk_out.stride_s;
+  P.gk_sh = b->dk_out.stride_h;
+  P.part = (float*)b->workspace;
+  P.dwq = P.wq ? b->dnorm_q : nullptr;
+  P.dwk = P.wk ? b->dnorm_k : nullptr;
+  if (fna2::launch_rope_norm_bwd(P, (hipStream_t)stream) != hipSuccess) return FNA2_E_LAUNCH;
   return FNA2_OK;
 }
 

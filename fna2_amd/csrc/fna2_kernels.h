@@ -56,11 +56,24 @@ struct RopeParams {
   const float* inv_freq;  // [D / 2]
   const void* q;
   const void* k;
-  void* q_out;
-  void* k_out;
+  void* q_out;  // forward: the rotated rows; backward: dq
+  void* k_out;  //                                       dk
   int64_t q_ss, q_sh, k_ss, k_sh, qo_ss, qo_sh, ko_ss, ko_sh;
+  const float* wq;  // RMSNorm weights [D] of q / k rows (null: no norm)
+  const float* wk;
+  float eps;
+  // backward of the normalised rotation: incoming gradients, dw partials
+  // [2][rope_blocks(T)][D] and the weight gradients
+  const void* gq;
+  const void* gk;
+  int64_t gq_ss, gq_sh, gk_ss, gk_sh;
+  float* part;
+  float* dwq;
+  float* dwk;
 };
+int rope_blocks(int T);  // workgroups of a rotary launch over T tokens
 hipError_t launch_rope(const RopeParams& P, hipStream_t s);
+hipError_t launch_rope_norm_bwd(const RopeParams& P, hipStream_t s);
 
 hipError_t launch_fwd(const FwdParams& P, int rp, int grid, hipStream_t s);
 hipError_t launch_bwd_dkdv(const BwdParams& P, int rpl, int grid, hipStream_t s);

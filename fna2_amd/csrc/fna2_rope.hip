@@ -34,6 +34,7 @@ namespace {
 constexpr int kRopeTokensPerWave = 4;
 constexpr int kRopeWaves = 4;
 constexpr int kRopePasses = 4;  // row passes whose loads are in flight together
+constexpr int kBwdPasses = 2;   // (the norm backward holds twice the data per pass)
 
 // Products and sums that are never fused into a multiply-add (the
 // reference evaluates them as separate elementwise ops).
@@ -104,79 +105,148 @@ struct Chunk {
   }
 };
 
+// Lane layout and the token -> sequence walk shared by the kernels: lane
+// owns columns [col, col + EPL) of both halves of row lrow + j * rpw of a
+// token; a wave covers kRopeTokensPerWave consecutive tokens from t0.
 template <int DT>
+struct RopeLanes {
+  static constexpr int EPL = Chunk<DT>::EPL;
+  int lane, half, lpr, rpw, col, lrow, nrows, t0, b;
+  __device__ __forceinline__ RopeLanes(const RopeParams& P, int wave_id) {
+    lane = threadIdx.x & 63;
+    half = P.D / 2;
+    lpr = half / EPL;  // lanes per row (divides 64)
+    rpw = 64 / lpr;    // rows per wave pass
+    col = (lane % lpr) * EPL;
+    lrow = lane / lpr;
+    nrows = P.Hq + P.Hk;
+    t0 = wave_id * kRopeTokensPerWave;
+    // Largest b with cu[b] <= t0 (b = -1: before the first sequence).
+    const auto cu = const_space(P.cu);
+    const int n = P.nseq;
+    int lo = -1, hi = n;  // cu[lo] <= t0 < cu[hi]
+    if (t0 < P.T) {
+      if (uni(cu[n]) <= t0) lo = n;
+      else
+        while (hi - lo > 1) {
+          const int mid = (lo + hi) >> 1;
+          if (uni(cu[mid]) <= t0) lo = mid;
+          else hi = mid;
+        }
+    }
+    b = lo;
+  }
+  // Step to token t; returns its position, or -1 outside every sequence.
+  __device__ __forceinline__ int position(const RopeParams& P, int t) {
+    const auto cu = const_space(P.cu);
+    while (b < P.nseq && uni(cu[b + 1]) <= t) ++b;
+    return (b >= 0 && b < P.nseq) ? t - uni(cu[b]) : -1;
+  }
+  // Row pointers (q rows first, then k rows).
+  __device__ __forceinline__ const char* in_row(const RopeParams& P, const void* q, const void* k,
+                                                int64_t qs, int64_t qh, int64_t ks, int64_t kh,
+                                                int t, int r) const {
+    constexpr int ES = DT == kRopeF32 ? 4 : 2;
+    const bool isq = r < P.Hq;
+    const int h = isq ? r : r - P.Hq;
+    return (const char*)(isq ? q : k) +
+           ((int64_t)t * (isq ? qs : ks) + (int64_t)h * (isq ? qh : kh)) * ES;
+  }
+};
+
+// Sum over the lpr lanes of a row (lanes lrow * lpr .. + lpr - 1); every
+// lane of the wave takes part.
+__device__ __forceinline__ float row_sum(float v, int lpr) {
+  for (int m = 1; m < lpr; m <<= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
+// Forward.  NORM: q and / or k rows are RMS-normalised first (weights wq /
+// wk; a null weight leaves those rows unnormalised), and the chain then runs
+// in fp32 with one rounding at the store.
+template <int DT, bool NORM>
 __global__ __launch_bounds__(64 * kRopeWaves) void rope_kernel(const RopeParams P) {
   using Ch = Chunk<DT>;
   constexpr int EPL = Ch::EPL;
-  constexpr int ES = DT == kRopeF32 ? 4 : 2;  // element bytes
-  const int lane = threadIdx.x & 63;
-  const int wv = uni(threadIdx.x >> 6);
-  const int half = P.D / 2;
-  const int lpr = half / EPL;   // lanes per row (divides 64)
-  const int rpw = 64 / lpr;     // rows per wave pass
-  const int col = (lane % lpr) * EPL;
-  const int lrow = lane / lpr;
-  const int nrows = P.Hq + P.Hk;
-  const int n = P.nseq;
-  const auto cu = const_space(P.cu);
+  constexpr int ES = DT == kRopeF32 ? 4 : 2;
+  constexpr int TD = NORM ? kRopeF32 : DT;  // type of the table and of the rotation
+  RopeLanes<DT> L(P, blockIdx.x * kRopeWaves + uni(threadIdx.x >> 6));
+  if (L.t0 >= P.T) return;
+  const int col = L.col, half = L.half;
 
   float invf[EPL];
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) invf[e] = rnd<DT>(P.inv_freq[col + e]);
-
-  const int t0 = (blockIdx.x * kRopeWaves + wv) * kRopeTokensPerWave;
-  if (t0 >= P.T) return;
-  // Largest b with cu[b] <= t0 (b = -1: before the first sequence).
-  int lo = -1, hi = n;  // cu[lo] <= t0 < cu[hi], with cu[-1] = -inf, cu[n + 1] = +inf
-  if (uni(cu[n]) <= t0) lo = n;
-  else
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (uni(cu[mid]) <= t0) lo = mid;
-      else hi = mid;
+  for (int e = 0; e < EPL; ++e) invf[e] = rnd<TD>(P.inv_freq[col + e]);
+  float wq1[NORM ? EPL : 1], wq2[NORM ? EPL : 1], wk1[NORM ? EPL : 1], wk2[NORM ? EPL : 1];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      wq1[e] = P.wq ? P.wq[col + e] : 1.f;
+      wq2[e] = P.wq ? P.wq[half + col + e] : 1.f;
+      wk1[e] = P.wk ? P.wk[col + e] : 1.f;
+      wk2[e] = P.wk ? P.wk[half + col + e] : 1.f;
     }
-  int b = lo;
+  }
+  const float inv_d = 1.f / (float)P.D;
 
   for (int i = 0; i < kRopeTokensPerWave; ++i) {
-    const int t = t0 + i;
+    const int t = L.t0 + i;
     if (t >= P.T) break;
-    while (b < n && uni(cu[b + 1]) <= t) ++b;
-    // inside a sequence: 0 <= b < n (cu[b] <= t < cu[b + 1])
-    const bool inside = b >= 0 && b < n;
+    const int p = L.position(P, t);
+    const bool inside = p >= 0;
     float c[EPL], s[EPL];
     if (inside) {
-      const float pos = rnd<DT>((float)(t - uni(cu[b])));
+      const float pos = rnd<TD>((float)p);
 #pragma unroll
       for (int e = 0; e < EPL; ++e) {
-        const float ang = rnd<DT>(mul_rn(pos, invf[e]));
+        const float ang = rnd<TD>(mul_rn(pos, invf[e]));
         float sv, cv;
         sincosf(ang, &sv, &cv);  // the accurate library routine
-        c[e] = rnd<DT>(cv);
-        s[e] = P.sign * rnd<DT>(sv);
+        c[e] = rnd<TD>(cv);
+        s[e] = P.sign * rnd<TD>(sv);
       }
     }
     // Four row passes at a time: every load first, then the arithmetic and
-    // the stores.
-    for (int r0 = lrow; r0 < nrows; r0 += kRopePasses * rpw) {
+    // the stores.  (With the norm every lane makes the same passes: the row
+    // sums cross lanes.)
+    for (int r0 = L.lrow; (NORM ? r0 - L.lrow : r0) < L.nrows; r0 += kRopePasses * L.rpw) {
       Ch x1[kRopePasses], x2[kRopePasses];
       char* dst[kRopePasses];
-      bool copy[kRopePasses];
+      bool copy[kRopePasses], isq[kRopePasses];
 #pragma unroll
       for (int j = 0; j < kRopePasses; ++j) {
-        const int r = r0 + j * rpw;
+        const int r = r0 + j * L.rpw;
         dst[j] = nullptr;
-        if (r < nrows) {
-          const bool isq = r < P.Hq;
-          const int h = isq ? r : r - P.Hq;
-          const char* src = (const char*)(isq ? P.q : P.k) +
-                            ((int64_t)t * (isq ? P.q_ss : P.k_ss) +
-                             (int64_t)h * (isq ? P.q_sh : P.k_sh)) * ES;
-          dst[j] = (char*)(isq ? P.q_out : P.k_out) +
-                   ((int64_t)t * (isq ? P.qo_ss : P.ko_ss) +
-                    (int64_t)h * (isq ? P.qo_sh : P.ko_sh)) * ES;
+        isq[j] = r < P.Hq;
+        if (r < L.nrows) {
+          const char* src = L.in_row(P, P.q, P.k, P.q_ss, P.q_sh, P.k_ss, P.k_sh, t, r);
+          dst[j] = (char*)L.in_row(P, P.q_out, P.k_out, P.qo_ss, P.qo_sh, P.ko_ss, P.ko_sh, t, r);
           copy[j] = dst[j] != src;
           x1[j].load(src + col * ES);
           x2[j].load(src + (half + col) * ES);
+        }
+      }
+      if constexpr (NORM) {
+        if (inside) {
+          // RMS of each row (every lane joins the cross-lane sums)
+#pragma unroll
+          for (int j = 0; j < kRopePasses; ++j) {
+            float ss = 0.f;
+            if (dst[j]) {
+#pragma unroll
+              for (int e = 0; e < EPL; ++e) ss += x1[j].v[e] * x1[j].v[e] + x2[j].v[e] * x2[j].v[e];
+            }
+            ss = row_sum(ss, L.lpr);
+            const bool has_w = isq[j] ? P.wq != nullptr : P.wk != nullptr;
+            if (dst[j] && has_w) {
+              const float rr = rsqrtf(ss * inv_d + P.eps);
+#pragma unroll
+              for (int e = 0; e < EPL; ++e) {
+                x1[j].v[e] = x1[j].v[e] * rr * (isq[j] ? wq1[e] : wk1[e]);
+                x2[j].v[e] = x2[j].v[e] * rr * (isq[j] ? wq2[e] : wk2[e]);
+              }
+            }
+          }
         }
       }
 #pragma unroll
@@ -186,10 +256,10 @@ __global__ __launch_bounds__(64 * kRopeWaves) void rope_kernel(const RopeParams 
           Ch y1, y2;
 #pragma unroll
           for (int e = 0; e < EPL; ++e) {
-            y1.v[e] = rnd<DT>(add_rn(rnd<DT>(mul_rn(x1[j].v[e], c[e])),
-                                     rnd<DT>(mul_rn(-x2[j].v[e], s[e]))));
-            y2.v[e] = rnd<DT>(add_rn(rnd<DT>(mul_rn(x2[j].v[e], c[e])),
-                                     rnd<DT>(mul_rn(x1[j].v[e], s[e]))));
+            y1.v[e] = rnd<TD>(add_rn(rnd<TD>(mul_rn(x1[j].v[e], c[e])),
+                                     rnd<TD>(mul_rn(-x2[j].v[e], s[e]))));
+            y2.v[e] = rnd<TD>(add_rn(rnd<TD>(mul_rn(x2[j].v[e], c[e])),
+                                     rnd<TD>(mul_rn(x1[j].v[e], s[e]))));
           }
           y1.store(dst[j] + col * ES);
           y2.store(dst[j] + (half + col) * ES);
@@ -202,18 +272,217 @@ __global__ __launch_bounds__(64 * kRopeWaves) void rope_kernel(const RopeParams 
   }
 }
 
+// Backward of the normalised rotation (fp32 chain, as the forward with a
+// norm): g' = R(-angle) dy, then for rows with a weight
+//     dx = r (w g') - x r^3 <x, w g'> / D,     dw += x r g'
+// (r = rsqrt(mean(x^2) + eps)); rows without one get dx = g'; tokens
+// outside every sequence pass dy through.  Each workgroup writes its dw
+// partial sums (fixed order) to part[2][gridDim.x][D].
+template <int DT>
+__global__ __launch_bounds__(64 * kRopeWaves) void rope_norm_bwd_kernel(const RopeParams P) {
+  using Ch = Chunk<DT>;
+  constexpr int EPL = Ch::EPL;
+  constexpr int ES = DT == kRopeF32 ? 4 : 2;
+  __shared__ float red[2][kRopeWaves][512];
+  const int wv = uni(threadIdx.x >> 6);
+  RopeLanes<DT> L(P, blockIdx.x * kRopeWaves + wv);
+  const int col = L.col, half = L.half, lane = L.lane;
+  float invf[EPL], wq1[EPL], wq2[EPL], wk1[EPL], wk2[EPL];
+  float aq1[EPL], aq2[EPL], ak1[EPL], ak2[EPL];  // dw partials of this lane's columns
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    invf[e] = P.inv_freq[col + e];
+    wq1[e] = P.wq ? P.wq[col + e] : 1.f;
+    wq2[e] = P.wq ? P.wq[half + col + e] : 1.f;
+    wk1[e] = P.wk ? P.wk[col + e] : 1.f;
+    wk2[e] = P.wk ? P.wk[half + col + e] : 1.f;
+    aq1[e] = aq2[e] = ak1[e] = ak2[e] = 0.f;
+  }
+  const float inv_d = 1.f / (float)P.D;
+
+  for (int i = 0; i < kRopeTokensPerWave && L.t0 < P.T; ++i) {
+    const int t = L.t0 + i;
+    if (t >= P.T) break;
+    const int p = L.position(P, t);
+    const bool inside = p >= 0;
+    float c[EPL], s[EPL];
+    if (inside) {
+      const float pos = (float)p;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        float sv, cv;
+        sincosf(mul_rn(pos, invf[e]), &sv, &cv);
+        c[e] = cv;
+        s[e] = P.sign * sv;
+      }
+    }
+    for (int r0 = L.lrow; r0 - L.lrow < L.nrows; r0 += kBwdPasses * L.rpw) {
+      Ch x1[kBwdPasses], x2[kBwdPasses], g1[kBwdPasses], g2[kBwdPasses];
+      char* dst[kBwdPasses];
+      bool isq[kBwdPasses];
+#pragma unroll
+      for (int j = 0; j < kBwdPasses; ++j) {
+        const int r = r0 + j * L.rpw;
+        dst[j] = nullptr;
+        isq[j] = r < P.Hq;
+        if (r < L.nrows) {
+          const char* xs = L.in_row(P, P.q, P.k, P.q_ss, P.q_sh, P.k_ss, P.k_sh, t, r);
+          const char* gs = L.in_row(P, P.gq, P.gk, P.gq_ss, P.gq_sh, P.gk_ss, P.gk_sh, t, r);
+          dst[j] = (char*)L.in_row(P, P.q_out, P.k_out, P.qo_ss, P.qo_sh, P.ko_ss, P.ko_sh, t, r);
+          x1[j].load(xs + col * ES);
+          x2[j].load(xs + (half + col) * ES);
+          g1[j].load(gs + col * ES);
+          g2[j].load(gs + (half + col) * ES);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kBwdPasses; ++j) {
+        if (inside) {
+          // g' = R(-angle) dy (the transpose of the forward rotation)
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) {
+            const float a = g1[j].v[e], bq = g2[j].v[e];
+            g1[j].v[e] = add_rn(mul_rn(a, c[e]), mul_rn(bq, s[e]));
+            g2[j].v[e] = add_rn(mul_rn(bq, c[e]), mul_rn(-a, s[e]));
+          }
+          float ss = 0.f, tw = 0.f;
+          if (dst[j]) {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+              const float w1 = isq[j] ? wq1[e] : wk1[e], w2 = isq[j] ? wq2[e] : wk2[e];
+              ss += x1[j].v[e] * x1[j].v[e] + x2[j].v[e] * x2[j].v[e];
+              tw += x1[j].v[e] * w1 * g1[j].v[e] + x2[j].v[e] * w2 * g2[j].v[e];
+            }
+          }
+          ss = row_sum(ss, L.lpr);
+          tw = row_sum(tw, L.lpr);
+          const bool has_w = isq[j] ? P.wq != nullptr : P.wk != nullptr;
+          if (dst[j] && has_w) {
+            const float rr = rsqrtf(ss * inv_d + P.eps);
+            const float k3 = rr * rr * rr * tw * inv_d;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+              const float w1 = isq[j] ? wq1[e] : wk1[e], w2 = isq[j] ? wq2[e] : wk2[e];
+              const float xr1 = x1[j].v[e] * rr, xr2 = x2[j].v[e] * rr;
+              if (isq[j]) aq1[e] += xr1 * g1[j].v[e], aq2[e] += xr2 * g2[j].v[e];
+              else ak1[e] += xr1 * g1[j].v[e], ak2[e] += xr2 * g2[j].v[e];
+              g1[j].v[e] = rr * w1 * g1[j].v[e] - x1[j].v[e] * k3;
+              g2[j].v[e] = rr * w2 * g2[j].v[e] - x2[j].v[e] * k3;
+            }
+          }
+        }
+        if (dst[j]) {
+          g1[j].store(dst[j] + col * ES);
+          g2[j].store(dst[j] + (half + col) * ES);
+        }
+      }
+    }
+  }
+
+  // dw partials: lanes sharing columns (lane % lpr), then the waves, in a
+  // fixed order.
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    for (int m = L.lpr; m < 64; m <<= 1) {
+      aq1[e] += __shfl_xor(aq1[e], m);
+      aq2[e] += __shfl_xor(aq2[e], m);
+      ak1[e] += __shfl_xor(ak1[e], m);
+      ak2[e] += __shfl_xor(ak2[e], m);
+    }
+  }
+  if (lane < L.lpr) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      red[0][wv][col + e] = aq1[e];
+      red[0][wv][half + col + e] = aq2[e];
+      red[1][wv][col + e] = ak1[e];
+      red[1][wv][half + col + e] = ak2[e];
+    }
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < 2 * P.D; d += 64 * kRopeWaves) {
+    const int which = d / P.D, dd = d - which * P.D;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < kRopeWaves; ++w) v += red[which][w][dd];
+    P.part[((int64_t)which * gridDim.x + blockIdx.x) * P.D + dd] = v;
+  }
+}
+
+// dw = sum over the workgroups' partials, in a fixed order: workgroup x
+// takes 64 of the 2 D columns (lane = column); its 16 waves sum interleaved
+// rows of partials (coalesced 256-byte rows), then wave 0 adds the 16 sums.
+__global__ __launch_bounds__(1024) void rope_dw_reduce_kernel(const RopeParams P, int nblocks) {
+  __shared__ float acc[16][64];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int d = blockIdx.x * 64 + lane;  // in [0, 2 D)
+  const bool ok = d < 2 * P.D;
+  const int which = ok ? d / P.D : 0, dd = ok ? d - which * P.D : 0;
+  const float* src = P.part + (int64_t)which * nblocks * P.D + dd;
+  float v = 0.f;
+  if (ok) {
+    int b = wv;
+    for (; b + 7 * 16 < nblocks; b += 8 * 16) {  // eight loads in flight
+      float t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = src[(int64_t)(b + 16 * u) * P.D];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v += t[u];
+    }
+    for (; b < nblocks; b += 16) v += src[(int64_t)b * P.D];
+  }
+  acc[wv][lane] = v;
+  __syncthreads();
+  if (wv == 0 && ok) {
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) s += acc[w][lane];
+    float* out = which == 0 ? P.dwq : P.dwk;
+    if (out) out[dd] = s;
+  }
+}
+
+}  // namespace
+
+int rope_blocks(int T) {
+  const int per_block = kRopeWaves * kRopeTokensPerWave;
+  return (T + per_block - 1) / per_block;
+}
+
+namespace {
+template <int DT>
+void launch_rope_dt(const RopeParams& P, dim3 grid, dim3 block, hipStream_t s) {
+  if (P.wq || P.wk)
+    hipLaunchKernelGGL((rope_kernel<DT, true>), grid, block, 0, s, P);
+  else
+    hipLaunchKernelGGL((rope_kernel<DT, false>), grid, block, 0, s, P);
+}
 }  // namespace
 
 hipError_t launch_rope(const RopeParams& P, hipStream_t s) {
   if (P.T <= 0 || P.Hq + P.Hk <= 0) return hipSuccess;
-  const int per_block = kRopeWaves * kRopeTokensPerWave;
-  const dim3 grid((P.T + per_block - 1) / per_block), block(64 * kRopeWaves);
+  const dim3 grid(rope_blocks(P.T)), block(64 * kRopeWaves);
   switch (P.dtype) {
-    case kRopeBF16: hipLaunchKernelGGL(rope_kernel<kRopeBF16>, grid, block, 0, s, P); break;
-    case kRopeF16: hipLaunchKernelGGL(rope_kernel<kRopeF16>, grid, block, 0, s, P); break;
-    case kRopeF32: hipLaunchKernelGGL(rope_kernel<kRopeF32>, grid, block, 0, s, P); break;
+    case kRopeBF16: launch_rope_dt<kRopeBF16>(P, grid, block, s); break;
+    case kRopeF16: launch_rope_dt<kRopeF16>(P, grid, block, s); break;
+    case kRopeF32: launch_rope_dt<kRopeF32>(P, grid, block, s); break;
     default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_norm_bwd(const RopeParams& P, hipStream_t s) {
+  if (P.T <= 0 || P.Hq + P.Hk <= 0) return hipSuccess;
+  const int nb = rope_blocks(P.T);
+  const dim3 grid(nb), block(64 * kRopeWaves);
+  switch (P.dtype) {
+    case kRopeBF16: hipLaunchKernelGGL(rope_norm_bwd_kernel<kRopeBF16>, grid, block, 0, s, P); break;
+    case kRopeF16: hipLaunchKernelGGL(rope_norm_bwd_kernel<kRopeF16>, grid, block, 0, s, P); break;
+    case kRopeF32: hipLaunchKernelGGL(rope_norm_bwd_kernel<kRopeF32>, grid, block, 0, s, P); break;
+    default: return hipErrorInvalidValue;
+  }
+  if (hipGetLastError() != hipSuccess) return hipErrorLaunchFailure;
+  hipLaunchKernelGGL(rope_dw_reduce_kernel, dim3((2 * P.D + 63) / 64), dim3(1024), 0, s, P, nb);
   return hipGetLastError();
 }
 

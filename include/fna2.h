@@ -156,7 +156,30 @@ typedef struct fna2_rope_args {
   const float* inv_freq;     /* [D/2] device fp32                           */
   fna2_tensor q, k;          /* [T, heads, D] (stride_s, stride_h)         */
   fna2_tensor q_out, k_out;  /* written; each equal to its input or disjoint */
+  /* Optional RMSNorm of every q / k row before the rotation (the reference's
+   * q_norm / k_norm, FNA2/attention_fna2.py:95-103, :558-561):
+   *     x <- x * rsqrt(mean(x^2) + norm_eps) * norm_[qk]
+   * NULL: that side is not normalised.  With a norm the whole chain is
+   * evaluated in fp32 and rounded once to the element type. */
+  const float* norm_q;       /* [D] fp32 or NULL                           */
+  const float* norm_k;       /* [D] fp32 or NULL                           */
+  float norm_eps;
 } fna2_rope_args;
+
+/* Backward of fna2_rope_varlen: dq and dk from the gradients of q_out and
+ * k_out, and (with a norm) the gradients of the norm weights.  Without a
+ * norm it is the inverse rotation (no workspace); with one it needs the
+ * forward's inputs (fwd.q, fwd.k) and fna2_rope_bwd_workspace_bytes of
+ * workspace, and sums the weight gradients in a fixed order. */
+typedef struct fna2_rope_bwd_args {
+  fna2_rope_args fwd;          /* the forward call's arguments              */
+  fna2_tensor dq_out, dk_out;  /* gradients of q_out and k_out              */
+  fna2_tensor dq, dk;          /* written (each equal to its gradient input or disjoint) */
+  float* dnorm_q;              /* [D] fp32, written when fwd.norm_q is set  */
+  float* dnorm_k;              /* [D] fp32, written when fwd.norm_k is set  */
+  void* workspace;
+  size_t workspace_bytes;
+} fna2_rope_bwd_args;
 
 /* Host-only validation of a rotary call (shapes, strides, alignment,
  * aliasing); no GPU call. */
@@ -164,6 +187,15 @@ int fna2_check_rope(const fna2_rope_args* args);
 
 /* Rotary embedding of q and k on the stream given (one launch). */
 int fna2_rope_varlen(const fna2_rope_args* args, void* hip_stream);
+
+/* Workspace bytes fna2_rope_bwd needs (0 without a norm). */
+size_t fna2_rope_bwd_workspace_bytes(const fna2_rope_args* fwd);
+
+/* Host-only validation of a rotary backward call; no GPU call. */
+int fna2_check_rope_bwd(const fna2_rope_bwd_args* args);
+
+/* Backward of fna2_rope_varlen (one launch without a norm, two with). */
+int fna2_rope_bwd(const fna2_rope_bwd_args* args, void* hip_stream);
 
 /* ABI version (FNA2_ABI_VERSION). */
 int fna2_version(void);

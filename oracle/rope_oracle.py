@@ -23,6 +23,14 @@ cos and sin are computed in float64 and rounded to fp32 first (an accurate
 fp32 routine), then to the dtype, as torch does for bf16/fp16 tensors.
 ``dtype = "f64"`` skips every rounding (exact rotation, for the invariants).
 
+* ``norm_rope_varlen``: ``RMSNorm`` (attention_fna2.py:95-103,
+  ``x * rsqrt(mean(x^2) + eps) * weight``) of every (token, head) row before
+  the rotation (``q_norm`` / ``k_norm`` then RoPE, :553-566), with the
+  angle table in fp32 (``table="f32"``: the reference's fp32 table; "f64":
+  exact angles) and the rest in float64, rounded once to the dtype: the
+  fused kernel computes the chain in fp32.  ``norm_rope_grads`` gives
+  its gradients (inputs and norm weights) for an upstream gradient.
+
 Pinning (tests/test_rope_oracle.py): the complex-multiplication form of the
 rotation, norm preservation and the relative-position property in f64, the
 identity at position 0, rotate/rotate-back, per-sequence restarts, the
@@ -112,3 +120,54 @@ def inv_freq_default(dim: int, base: float = 10000.0) -> np.ndarray:
     """1 / base^(2i/dim) as the fp32 buffer of attention_fna2.py:121-122."""
     i = np.arange(0, dim, 2, dtype=np.float32)
     return (1.0 / (np.float32(base) ** (i / np.float32(dim)))).astype(np.float32)
+
+
+def _rms_norm(x, w, eps):
+    x = np.asarray(x, dtype=np.float64)
+    r = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    return x * r * np.asarray(w, dtype=np.float64), r
+
+
+def norm_rope_varlen(q, k, cu_seqlens, inv_freq, wq, wk, eps: float, dtype: str,
+                     table: str = "f32"):
+    """RMSNorm (weights wq / wk, None: no norm) then the rotation, in float64
+    with the angle table in ``table`` precision, rounded once to the dtype.
+    Tokens outside every sequence unchanged."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    pos, inside = positions(cu_seqlens, q.shape[0])
+    c, s = cos_sin(pos, inv_freq, table)
+    out = []
+    for x, w in ((q, wq), (k, wk)):
+        xn = x if w is None else _rms_norm(x, w, eps)[0]
+        y = round_to(rotate(xn, c, s, "f64"), dtype)
+        out.append(np.where(inside[:, None, None], y, x))
+    return out[0], out[1]
+
+
+def norm_rope_grads(q, k, cu_seqlens, inv_freq, wq, wk, eps: float, gq, gk,
+                    table: str = "f32"):
+    """Gradients of sum(gq * y_q) + sum(gk * y_k) for y = rotate(RMSNorm(x)):
+    (dq, dk, dwq, dwk) in float64.  dx = r (w . g') - x r^3 <x, w . g'> / D with
+    g' = rotate^-1(g); dw = sum over rows of x r g'.  Outside tokens pass the
+    gradient through unchanged (and add nothing to dw)."""
+    pos, inside = positions(cu_seqlens, np.asarray(q).shape[0])
+    c, s = cos_sin(pos, inv_freq, table)
+    res = []
+    for x, w, g in ((q, wq, gq), (k, wk, gk)):
+        x = np.asarray(x, dtype=np.float64)
+        g = np.asarray(g, dtype=np.float64)
+        gr = rotate(g, c, s, "f64", sign=-1)  # the rotation's transpose
+        if w is None:
+            dx, dw = gr, None
+        else:
+            w = np.asarray(w, dtype=np.float64)
+            D = x.shape[-1]
+            r = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+            wg = w * gr
+            dx = r * wg - x * r ** 3 * np.sum(x * wg, axis=-1, keepdims=True) / D
+            dw = np.sum(np.where(inside[:, None, None], x * r * gr, 0.0), axis=(0, 1))
+        dx = np.where(inside[:, None, None], dx, g)
+        res.append((dx, dw))
+    return res[0][0], res[1][0], res[0][1], res[1][1]
+

@@ -48,6 +48,35 @@ def _check(lib, a):
     return _capi.STATUS[lib.fna2_check_rope(ctypes.byref(a))]
 
 
+def _bwd(lib, **over):
+    b = _capi.RopeBwdArgs()
+    b.fwd = _args()
+    b.fwd.norm_q, b.fwd.norm_eps = FAKE, 1e-6
+    b.dq_out = _capi.Tensor(FAKE + (4 << 24), 0, 4 * 128, 128)
+    b.dk_out = _capi.Tensor(FAKE + (5 << 24), 0, 2 * 128, 128)
+    b.dq = _capi.Tensor(FAKE + (6 << 24), 0, 4 * 128, 128)
+    b.dk = _capi.Tensor(FAKE + (7 << 24), 0, 2 * 128, 128)
+    b.dnorm_q = FAKE
+    b.workspace, b.workspace_bytes = FAKE, 1 << 30
+    for k, v in over.items():
+        setattr(b, k, v)
+    return _capi.STATUS[lib.fna2_check_rope_bwd(ctypes.byref(b))]
+
+
+def test_check_rope_bwd(lib):
+    assert _bwd(lib) == "FNA2_OK"
+    assert _bwd(lib, workspace=None) == "FNA2_E_WORKSPACE"
+    assert _bwd(lib, workspace_bytes=16) == "FNA2_E_WORKSPACE"
+    assert _bwd(lib, dnorm_q=None) == "FNA2_E_NULL"
+    assert _bwd(lib, dq=_capi.Tensor(FAKE + (4 << 24) + 256, 0, 4 * 128, 128)) == "FNA2_E_ALIAS"
+    a = _args()
+    assert lib.fna2_rope_bwd_workspace_bytes(ctypes.byref(a)) == 0  # no norm: none
+    a.norm_k, a.norm_eps = FAKE, 1e-6
+    assert lib.fna2_rope_bwd_workspace_bytes(ctypes.byref(a)) >= 2 * 4 * 128 * 4
+    a.norm_eps = float("nan")
+    assert _check(lib, a) == "FNA2_E_SCALE"
+
+
 def test_check_rope_accepts(lib):
     assert _check(lib, _args()) == "FNA2_OK"
     assert _check(lib, _args(dtype=3, head_dim=64)) == "FNA2_OK"
@@ -197,3 +226,52 @@ def test_headline_size_round_trip(gpu):
     pos0[cu_t[:-1].long()] = True
     assert torch.equal(yq[pos0], q[pos0])
     assert (yq[~pos0] - q[~pos0]).abs().max().item() > 0.1
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("which", ["both", "q"])
+def test_norm_rope_forward_backward(gpu, dtype, which):
+    """QK-RMSNorm + RoPE in one launch, and its backward (inputs and norm
+    weights), against the oracle: fp32 chain rounded once (forward); float64
+    gradients on the same (rounded) inputs."""
+    from fna2_amd.rope import rope_varlen
+    lens = [300, 0, 1, 77, 500]
+    cu = [3] + list(3 + np.cumsum(lens))
+    T, D = cu[-1] + 5, 128
+    q, k, cu_t, inv = _case(T, 4, 2, D, cu, dtype, 30, gpu)
+    g = torch.Generator().manual_seed(31)
+    wq = (1 + 0.3 * torch.randn(D, generator=g)).to(gpu)
+    wk = (1 + 0.3 * torch.randn(D, generator=g)).to(gpu) if which == "both" else None
+    gq = torch.randn(q.shape, generator=g).to(dtype).to(gpu)
+    gk = torch.randn(k.shape, generator=g).to(dtype).to(gpu)
+    leaves = [q.clone().requires_grad_(True), k.clone().requires_grad_(True),
+              wq.clone().requires_grad_(True)] + ([wk.clone().requires_grad_(True)] if wk is not None else [])
+    print(f"norm rope dtype={dtype} which={which}", flush=True)
+    yq, yk = rope_varlen(leaves[0], leaves[1], cu_t, inv.to(gpu), leaves[2],
+                         leaves[3] if wk is not None else None, 1e-6)
+    grads = torch.autograd.grad([yq, yk], leaves, [gq, gk])
+    torch.cuda.synchronize()
+    npy = lambda t: None if t is None else t.detach().float().cpu().numpy()
+    wq_n, wk_n = npy(wq), npy(wk)
+    fq, fk = RO.norm_rope_varlen(npy(q), npy(k), cu, inv.numpy(), wq_n, wk_n, 1e-6, DT[dtype])
+    _compare_loose = (lambda got, want: np.testing.assert_allclose(
+        got.detach().float().cpu().numpy(), want, rtol=0,
+        atol=1e-5 if dtype == torch.float32 else 1.5e-2))
+    _compare_loose(yq, fq)
+    _compare_loose(yk, fk)
+    dq, dk, dwq, dwk = RO.norm_rope_grads(npy(q), npy(k), cu, inv.numpy(), wq_n, wk_n, 1e-6,
+                                          npy(gq), npy(gk))
+    rel = lambda got, want: np.linalg.norm(npy(got) - want) / np.linalg.norm(want)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert rel(grads[0], dq) < tol and rel(grads[1], dk) < tol
+    assert rel(grads[2], dwq) < tol
+    if wk is not None:
+        assert rel(grads[3], dwk) < tol
+    # determinism of the weight gradients (fixed-order sums)
+    grads2 = torch.autograd.grad(list(rope_varlen(leaves[0], leaves[1], cu_t, inv.to(gpu), leaves[2],
+                                                  leaves[3] if wk is not None else None, 1e-6)),
+                                 leaves, [gq, gk])
+    for a, b in zip(grads, grads2):
+        assert torch.equal(a, b)
+

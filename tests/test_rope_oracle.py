@@ -164,3 +164,79 @@ def test_planted_mistake_is_caught(monkeypatch):
     monkeypatch.setattr(RO, "rotate", bad)
     with pytest.raises(AssertionError):
         test_complex_form_f64()
+
+
+# ── QK-RMSNorm + RoPE (oracle.rope_oracle.norm_rope_varlen / norm_rope_grads) ──
+
+def _norm_case(seed=20):
+    rng = np.random.default_rng(seed)
+    T, D = 30, 16
+    q, k = rng.standard_normal((T, 3, D)), rng.standard_normal((T, 2, D))
+    wq, wk = rng.standard_normal(D), rng.standard_normal(D)
+    return q, k, wq, wk, [2, 12, 25], RO.inv_freq_default(D)
+
+
+def _torch_norm_rope(qt, kt, wqt, wkt, cu, inv, eps, table_dtype=torch.float64):
+    """The reference chain (attention_fna2.py:95-103 then :163-170) in torch."""
+    T, D = qt.shape[0], qt.shape[-1]
+    pos, inside = RO.positions(cu, T)
+    ang = torch.outer(torch.tensor(pos, dtype=table_dtype), torch.tensor(inv).to(table_dtype))
+    c, s = ang.cos().to(qt.dtype)[:, None, :], ang.sin().to(qt.dtype)[:, None, :]
+    out = []
+    for x, w in ((qt, wqt), (kt, wkt)):
+        xn = x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps) * w
+        h = D // 2
+        y = torch.cat([xn[..., :h] * c - xn[..., h:] * s, xn[..., h:] * c + xn[..., :h] * s], -1)
+        out.append(torch.where(torch.tensor(inside)[:, None, None], y, x))
+    return out
+
+
+def test_norm_rope_grads_match_torch_autograd():
+    q, k, wq, wk, cu, inv = _norm_case()
+    rng = np.random.default_rng(21)
+    gq, gk = rng.standard_normal(q.shape), rng.standard_normal(k.shape)
+    dq, dk, dwq, dwk = RO.norm_rope_grads(q, k, cu, inv, wq, wk, 1e-6, gq, gk, table="f64")
+    ts = [torch.tensor(a, requires_grad=True) for a in (q, k, wq, wk)]
+    yq, yk = _torch_norm_rope(*ts, cu, inv, 1e-6)
+    # the forward agrees too (f64 table)
+    fq, fk = RO.norm_rope_varlen(q, k, cu, inv, wq, wk, 1e-6, "f64", table="f64")
+    np.testing.assert_allclose(fq, yq.detach().numpy(), atol=1e-12)
+    g = torch.autograd.grad([yq, yk], ts, [torch.tensor(gq), torch.tensor(gk)])
+    for a, b in zip((dq, dk, dwq, dwk), g):
+        np.testing.assert_allclose(a, b.numpy(), atol=1e-12)
+
+
+def test_norm_rope_matches_torch_fp32_chain():
+    """fp32 table at positions up to 700 (where an exact-angle table would
+    differ by ~1e-5)."""
+    rng = np.random.default_rng(22)
+    q, k = rng.standard_normal((700, 2, 16)), rng.standard_normal((700, 1, 16))
+    wq, wk = rng.standard_normal(16), rng.standard_normal(16)
+    cu, inv = [0, 700], RO.inv_freq_default(16)
+    ts = [torch.tensor(a, dtype=torch.float32) for a in (q, k, wq, wk)]
+    yq, yk = _torch_norm_rope(*ts, cu, inv, 1e-6, table_dtype=torch.float32)
+    fq, fk = RO.norm_rope_varlen(q.astype(np.float32), k.astype(np.float32), cu, inv,
+                                 wq.astype(np.float32), wk.astype(np.float32), 1e-6, "f32")
+    np.testing.assert_allclose(fq, yq.numpy(), atol=5e-6)
+    np.testing.assert_allclose(fk, yk.numpy(), atol=5e-6)
+
+
+def test_norm_rope_scale_invariant():
+    q, k, wq, wk, cu, inv = _norm_case(23)
+    a = RO.norm_rope_varlen(q, k, cu, inv, wq, wk, 0.0, "f64", table="f64")
+    b = RO.norm_rope_varlen(3.7 * q, 0.2 * k, cu, inv, wq, wk, 0.0, "f64", table="f64")
+    pos, inside = RO.positions(cu, q.shape[0])
+    np.testing.assert_allclose(a[0][inside], b[0][inside], atol=1e-12)
+    np.testing.assert_allclose(a[1][inside], b[1][inside], atol=1e-12)
+
+
+def test_norm_rope_planted_mistake_is_caught(monkeypatch):
+    """A dropped 1/D in the norm gradient must fail the autograd check."""
+    good = RO.norm_rope_grads
+
+    def bad(q, k, cu, inv, wq, wk, eps, gq, gk, table="f32"):
+        dq, dk, dwq, dwk = good(q, k, cu, inv, wq, wk, eps, gq, gk, table)
+        return dq * 1.01, dk, dwq, dwk
+    monkeypatch.setattr(RO, "norm_rope_grads", bad)
+    with pytest.raises(AssertionError):
+        test_norm_rope_grads_match_torch_autograd()
