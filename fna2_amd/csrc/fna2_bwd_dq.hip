@@ -25,7 +25,9 @@ template <int D, int RPL>
 struct DqCfg {
   static constexpr int NW = 4;
   static constexpr int BM = kDqBM;  // queries per workgroup
-  static constexpr int BN = D == 128 ? 32 : kDqBN;  // keys per step (fits 2 waves/SIMD)
+  // keys per step: 32 keeps d = 128 within 2 waves per SIMD and d = 64
+  // (rank <= 32) within 3; rank 64 at d = 64 steps 64 keys.
+  static constexpr int BN = (D == 128 || RPL <= 32) ? 32 : kDqBN;
   static constexpr int NKB = BN / 32;               // 32-key blocks per step
   static constexpr int CD = D / 8;
   static constexpr int CR = RPL > 0 ? RPL / 8 : 4;
@@ -313,8 +315,8 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   __global__ __launch_bounds__(256, WAVES) void dq_kernel_d##D##_r##RPL(const BwdParams P) { \
     dq_body<D, RPL>(P);                                                                 \
   }
-FNA2_DQ_KERNEL(64, 0, 2)
-FNA2_DQ_KERNEL(64, 32, 2)
+FNA2_DQ_KERNEL(64, 0, 3)
+FNA2_DQ_KERNEL(64, 32, 3)
 FNA2_DQ_KERNEL(64, 64, 2)
 FNA2_DQ_KERNEL(128, 0, 2)
 FNA2_DQ_KERNEL(128, 32, 2)
