@@ -55,6 +55,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--rope", action="store_true",
                     help="measure the varlen RoPE kernel (c3 pack) instead of attention")
+    ap.add_argument("--decode", action="store_true",
+                    help="bench the KV-cache decode kernel instead of the training step")
     ap.add_argument("--producer", action="store_true",
                     help="measure the fused operand projection (c3-sized module) instead")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
@@ -495,8 +497,155 @@ def producer_bench(args):
     }), flush=True)
 
 
+def decode_bench(args):
+    """One-token decode against a KV cache, with c3's attention geometry
+    (16 heads of 128, all graph heads of rank 32), 64 sequences x 4096
+    cached rows, bf16; plus a grouped-query variant (32 query heads on 8 KV
+    heads)."""
+    import ctypes
+
+    import torch
+    import torch.nn.functional as Fn
+
+    from fna2_amd import _capi
+    from fna2_amd.decode import decode_args
+
+    lib = _capi.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    def inputs(B, H, HKV, HG, D, R, L, seed=42):
+        g = torch.Generator().manual_seed(seed)
+        draw = lambda *s, std=1.0: (torch.randn(*s, generator=g) * std).bfloat16().to(dev)
+        return (draw(B, H, D), draw(B, HKV, L, D), draw(B, HKV, L, D), draw(B, HG, R, std=R ** -0.5),
+                draw(B, HG, L, R, std=R ** -0.5), torch.randn(HG, generator=g).float().to(dev))
+
+    def measure(shape, bias, steps, warmup):
+        B, H, HKV, HG, D, R, L = shape
+        q, k, v, rq, rk, gs = inputs(*shape)
+        scale = D ** -0.5
+        a, keep, out, lse = decode_args(q, k, v, rq if bias else None, rk if bias else None,
+                                        gs if bias else None, scale)
+        nws = lib.fna2_decode_workspace_bytes(ctypes.byref(a))
+        ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), nws
+        call = lambda: _capi.raise_for(lib.fna2_decode(ctypes.byref(a), stream), "fna2_decode")
+        for _ in range(warmup):
+            call()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        # the split kernel alone: events the library records around it
+        pool = [torch.cuda.Event(enable_timing=True) for _ in range(2 * steps)]
+        for ev in pool:
+            ev.record()
+        torch.cuda.synchronize()
+        for i in range(steps):
+            evs = (ctypes.c_void_p * 2)(pool[2 * i].cuda_event, pool[2 * i + 1].cuda_event)
+            a.events = ctypes.cast(evs, ctypes.c_void_p)
+            call()
+        torch.cuda.synchronize()
+        a.events = None
+        k_ms = statistics.mean(pool[2 * i].elapsed_time(pool[2 * i + 1]) for i in range(steps))
+        nbytes = B * HKV * L * D * 2 * 2 + (B * HG * L * R * 2 if bias else 0) \
+            + 2 * B * H * D * 2 + (B * HG * R * 2 if bias else 0)
+        # the reference's decode step on the same cache: SDPA over the cached
+        # rows (attention_fna2.py:445-473, torch.cat of the cache not timed),
+        # and the same with the graph bias as an explicit mask
+        G = H // HKV
+        ke = k.repeat_interleave(G, dim=1) if G > 1 else k
+        ve = v.repeat_interleave(G, dim=1) if G > 1 else v
+        q4 = q[:, :, None]
+
+        def eager():
+            if G > 1:  # the reference expands K / V every step
+                kk, vv = k.repeat_interleave(G, dim=1), v.repeat_interleave(G, dim=1)
+            else:
+                kk, vv = ke, ve
+            mask = None
+            if bias:
+                b = torch.matmul(rq[:, :, None].float(), rk.float().transpose(-2, -1).contiguous())
+                mask = (gs.view(1, -1, 1, 1) * b).to(torch.bfloat16)
+                if HG < H:
+                    mask = torch.cat([mask, mask.new_zeros(B, H - HG, 1, L)], dim=1)
+            return Fn.scaled_dot_product_attention(q4, kk, vv, attn_mask=mask, scale=scale)
+        for _ in range(3):
+            eager()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        n_e = max(steps // 4, 5)
+        for _ in range(n_e):
+            eager()
+        torch.cuda.synchronize()
+        ms_eager = (time.perf_counter() - t0) / n_e * 1e3
+        del keep
+        return dict(ms=ms, kernel_ms=k_ms, bytes=nbytes, eager_ms=ms_eager,
+                    splits=lib.fna2_decode_num_splits(ctypes.byref(a)),
+                    inputs=(q, k, v, rq, rk, gs, scale))
+
+    main_shape = (64, 16, 16, 16, 128, 32, 4096)
+    gqa_shape = (64, 32, 8, 32, 128, 32, 4096)
+    r = measure(main_shape, True, args.steps, args.warmup)
+    r0 = measure(main_shape, False, args.steps, args.warmup)
+    rg = measure(gqa_shape, True, args.steps, args.warmup)
+    gbs = r["bytes"] / (r["ms"] * 1e-3) / 1e9
+    kgbs = r["bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
+    line = {
+        "metric": "decode HBM GB/s (K, V and Rk cache read once per step)",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(r["ms"], 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q and caches, R ~ N(0, 1/R))",
+        "config": {"workload": "decode: 64 sequences x 4096 cached rows, 16 heads (all graph "
+                               "heads, R=32), 16 KV heads, d=128 (c3's attention geometry)",
+                   "num_splits": r["splits"]},
+        "roofline": {"bound": "hbm", "achieved": round(kgbs, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(kgbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "decode_kernel_d128_c4", "algorithmic_bytes": r["bytes"],
+                     "kernel_ms": round(r["kernel_ms"], 5)},
+        "eager_reference_ms": {"with_bias": round(r["eager_ms"], 4),
+                               "without_bias": round(r0["eager_ms"], 4)},
+        "speedup_over_eager": round(r["eager_ms"] / r["ms"], 2),
+        "without_bias": {"ms": round(r0["ms"], 5),
+                         "GBps": round(r0["bytes"] / (r0["ms"] * 1e-3) / 1e9, 1),
+                         "speedup_over_reference_sdpa": round(r0["eager_ms"] / r0["ms"], 2)},
+        "gqa_32q_8kv": {"ms": round(rg["ms"], 5), "kernel_ms": round(rg["kernel_ms"], 5),
+                        "GBps": round(rg["bytes"] / (rg["ms"] * 1e-3) / 1e9, 1),
+                        "kernel_GBps": round(rg["bytes"] / (rg["kernel_ms"] * 1e-3) / 1e9, 1),
+                        "eager_ms": round(rg["eager_ms"], 4), "num_splits": rg["splits"]},
+    }
+    if not args.no_cpu:
+        from oracle import fna2_oracle as O
+        q, k, v, rq, rk, gs, scale = r["inputs"]
+        n = 4  # leading sequences
+        host = [t[:n].float().cpu().numpy() for t in (q, k, v, rq, rk)]
+        gsh = gs.cpu().numpy()
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            O.decode(*host[:3], host[3], host[4], gsh, scale)
+            ts.append(time.perf_counter() - t0)
+        med = statistics.median(ts)
+        line["cpu_baseline"] = {"value": round(r["bytes"] * n / 64 / med / 1e9, 3),
+                                "unit": "GB/s", "cores": 1, "kind": "port",
+                                "sample": f"oracle.decode (numpy, fp64) on the first {n} of 64 "
+                                          f"sequences, median of 3: {med * 1e3:.1f} ms"}
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
+    if args.decode:
+        decode_bench(args)
+        return
     if args.producer:
         producer_bench(args)
         return

@@ -90,6 +90,7 @@ class FwdArgs(ctypes.Structure):
 
 FWD_EVENTS = 2
 BWD_EVENTS = 4
+DECODE_EVENTS = 2
 
 
 class BwdArgs(ctypes.Structure):
@@ -152,6 +153,32 @@ class RopeBwdArgs(ctypes.Structure):
     ]
 
 
+class DecodeArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("heads_kv", ctypes.c_int32),
+        ("heads_graph", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("rank", ctypes.c_int32),
+        ("max_seqlen_k", ctypes.c_int32),
+        ("num_splits", ctypes.c_int32),
+        ("softmax_scale", ctypes.c_float),
+        ("seqlens_k", ctypes.c_void_p),
+        ("q", Tensor),
+        ("r_q", Tensor),
+        ("k_cache", Tensor),
+        ("v_cache", Tensor),
+        ("rk_cache", Tensor),
+        ("graph_scale", ctypes.c_void_p),
+        ("out", Tensor),
+        ("lse", Tensor),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("events", ctypes.c_void_p),
+    ]
+
+
 # Every symbol the header declares, with its ctypes signature.
 SIGNATURES = {
     "fna2_version": (ctypes.c_int, []),
@@ -167,6 +194,10 @@ SIGNATURES = {
     "fna2_rope_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(RopeArgs)]),
     "fna2_check_rope_bwd": (ctypes.c_int, [ctypes.POINTER(RopeBwdArgs)]),
     "fna2_rope_bwd": (ctypes.c_int, [ctypes.POINTER(RopeBwdArgs), ctypes.c_void_p]),
+    "fna2_check_decode": (ctypes.c_int, [ctypes.POINTER(DecodeArgs)]),
+    "fna2_decode_num_splits": (ctypes.c_int, [ctypes.POINTER(DecodeArgs)]),
+    "fna2_decode_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(DecodeArgs)]),
+    "fna2_decode": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), ctypes.c_void_p]),
 }
 
 _lib = None

@@ -8,11 +8,16 @@ The module keeps the reference's constructor and ``forward`` signatures
   ``[T, E]`` with ``cu_seqlens_q/k``) -- runs ``flash_naylis_attn``, i.e. the
   gfx950 HIP kernels, with ``R_q``/``R_k`` of shape ``[B, H_G, S, R]`` /
   ``[T, H_G, R]`` and ``graph_scale`` in fp32;
-* the paths the reference sends elsewhere keep going elsewhere: decode with a
-  KV cache, ``soft_cap`` and modules built with ``use_fna2=False`` use
-  PyTorch's SDPA with a materialised bias, or the explicit softmax when a
-  ``soft_cap`` or custom ``mask`` is given (attention_fna2.py:337-374,
-  :493-516).
+* decoding one token against a KV cache runs the gfx950 decode kernel
+  (``flash_naylis_decode``) where the reference runs SDPA over
+  ``torch.cat(past_kv, new)`` (:412-429, :445-473): the same result, without
+  the graph bias, as there.  ``decode_graph_bias=True`` (an extra keyword)
+  keeps ``R_k`` in the cache, ``(k, v, r_k)``, and decodes with the bias, so
+  that a decode step equals the last row of the full causal forward;
+* the other paths the reference sends elsewhere keep going elsewhere:
+  ``soft_cap`` and modules built with ``use_fna2=False`` use PyTorch's SDPA
+  with a materialised bias, or the explicit softmax when a ``soft_cap`` or
+  custom ``mask`` is given (attention_fna2.py:337-374, :493-516).
 
 ``_FNA2_AVAILABLE`` is true when the HIP library loads and the current device
 is gfx950.  A module asks for FNA2 with ``use_fna2=None`` (auto) or ``True``;
@@ -36,6 +41,7 @@ import torch.nn.functional as F
 
 from . import _capi
 from .flash_naylis_attn import BLOCK_R, flash_naylis_attn, rank_supported
+from .decode import flash_naylis_decode
 from .rope import rope_varlen
 
 
@@ -54,7 +60,8 @@ _FNA2_AVAILABLE = _detect_fna2()
 _FNA2_BLOCK_R = BLOCK_R
 _flash_naylis_attn = flash_naylis_attn
 
-KVCache = Tuple[torch.Tensor, torch.Tensor]
+# (k, v), or (k, v, r_k) for a module built with decode_graph_bias=True.
+KVCache = Tuple[torch.Tensor, ...]
 
 
 class RMSNorm(nn.Module):
@@ -155,6 +162,7 @@ class NaylisAttention(nn.Module):
         sym_heads: int = 0,
         vanilla_heads: int = 0,
         use_fna2: Optional[bool] = None,
+        decode_graph_bias: bool = False,
     ):
         super().__init__()
         assert embed_dim % num_heads == 0
@@ -205,6 +213,10 @@ class NaylisAttention(nn.Module):
             self.rel_q_proj = self.rel_k_proj = None
             self.graph_scale = None
         self._sdpa_ok = hasattr(F, "scaled_dot_product_attention")
+        # Keep R_k in the KV cache, (k, v, r_k), and decode with the graph
+        # bias (the reference's cache is (k, v) and its decode step drops the
+        # bias).
+        self.decode_graph_bias = bool(decode_graph_bias) and graph_heads > 0
 
     # ── helpers ────────────────────────────────────────────────────────────
     def _attn_scale(self) -> float:
@@ -280,14 +292,26 @@ class NaylisAttention(nn.Module):
                                         max_seqlen_k)
         B, S, _ = x.shape
         scale = self._attn_scale()
+        keep_rk = self.decode_graph_bias
+        if keep_rk and past_kv is not None and len(past_kv) < 3:
+            raise ValueError("decode_graph_bias: past_kv must be the (k, v, r_k) cache "
+                             "this module returns")
         fused = (self._use_fna2 and self.graph_heads > 0 and self.soft_cap is None
                  and past_kv is None)
-        if fused:
+        # One new token against a cache: the decode kernel (attention_fna2.py
+        # :412-429 decodes with SDPA over torch.cat(past_kv, new)).
+        kernel_decode = (self._use_fna2 and past_kv is not None and S == 1
+                         and self.soft_cap is None
+                         and not (self.training and self.dropout.p > 0))
+        r_q = r_k = None
+        if fused or kernel_decode:
             q, k, v, r_q, r_k = self._project(x)
         else:
             q = self.q_proj(x).view(B, S, self.num_heads, self.head_dim).transpose(1, 2)
             k = self.k_proj(x).view(B, S, self.n_kv_heads, self.head_dim).transpose(1, 2)
             v = self.v_proj(x).view(B, S, self.n_kv_heads, self.head_dim).transpose(1, 2)
+            if keep_rk:
+                r_q, r_k = self._rel(x)
         if self.use_qk_norm:
             q, k = self.q_norm(q), self.k_norm(k)
         offset = past_kv[0].shape[2] if past_kv is not None else 0
@@ -296,30 +320,61 @@ class NaylisAttention(nn.Module):
         if past_kv is not None:
             k = torch.cat([past_kv[0], k], dim=2)
             v = torch.cat([past_kv[1], v], dim=2)
-        new_cache: Optional[KVCache] = (k, v) if use_kv_cache else None
+            if keep_rk:
+                r_k = torch.cat([past_kv[2], r_k], dim=2)
+        new_cache: Optional[KVCache] = None
+        if use_kv_cache:
+            new_cache = (k, v, r_k.contiguous()) if keep_rk else (k, v)
 
         orig_dtype = q.dtype
         if q.dtype == torch.float32:
             q, k, v = (t.to(torch.bfloat16) for t in (q, k, v))
         is_causal = S > 1 and past_kv is None
         use_graph = self.graph_heads > 0 and (S > 1 or past_kv is None)
+        cached_bias = keep_rk and past_kv is not None and S == 1
 
         if fused:
             out = _flash_naylis_attn(q, k, v, r_q, r_k, self.graph_scale.to(torch.float32),
                                      softmax_scale=scale, is_causal=is_causal)
+        elif kernel_decode:
+            out = flash_naylis_decode(
+                q, k, v, r_q if cached_bias else None, r_k if cached_bias else None,
+                self.graph_scale if cached_bias else None, softmax_scale=scale).unsqueeze(2)
         else:
-            out = self._attend_eager(x, q, k, v, mask, past_kv, scale, is_causal, use_graph)
+            bias = self._cached_bias(r_q, r_k, q.dtype) if cached_bias else None
+            out = self._attend_eager(x, q, k, v, mask, past_kv, scale, is_causal, use_graph,
+                                     bias)
         out = out.transpose(1, 2).contiguous().view(B, S, self.embed_dim)
         return self._finish(out, orig_dtype), new_cache
 
-    def _attend_eager(self, x, q, k, v, mask, past_kv, scale, is_causal, use_graph):
+    def _rel(self, x: torch.Tensor):
+        """R_q, R_k [B, H_G, S, R] in bf16 (attention_fna2.py:301-318)."""
+        B, S, _ = x.shape
+        r_q = self.rel_q_proj(x).view(B, S, self.graph_heads, self.rel_rank).transpose(1, 2)
+        r_k = self.rel_k_proj(x).view(B, S, self.graph_heads, self.rel_rank).transpose(1, 2)
+        return r_q.to(torch.bfloat16), r_k.to(torch.bfloat16)
+
+    def _cached_bias(self, r_q, rk_cache, dtype) -> torch.Tensor:
+        """gs_h <Rq_new, Rk_j> against the cached rows, [B, H, 1, L] (zeros
+        for vanilla heads), for the eager backends."""
+        bias = torch.matmul(r_q.float(), rk_cache.float().transpose(-2, -1).contiguous())
+        bias = (self.graph_scale.float().view(1, -1, 1, 1) * bias).to(dtype)
+        if self.vanilla_heads > 0:
+            B, _, _, L = bias.shape
+            bias = torch.cat([bias, bias.new_zeros(B, self.vanilla_heads, 1, L)], dim=1)
+        return bias
+
+    def _attend_eager(self, x, q, k, v, mask, past_kv, scale, is_causal, use_graph,
+                      bias=None):
         """The reference's non-FNA2 backends: SDPA with a dense bias, or the
-        explicit softmax for soft_cap (attention_fna2.py:449-516)."""
+        explicit softmax for soft_cap (attention_fna2.py:449-516).  ``bias``:
+        a precomputed additive bias (decoding against a cache with R_k)."""
         if self.n_kv_heads != self.num_heads:
             k = k.repeat_interleave(self.num_queries_per_kv, dim=1)
             v = v.repeat_interleave(self.num_queries_per_kv, dim=1)
         p_drop = self.dropout.p if self.training else 0.0
-        bias = self._dense_bias(x, q.dtype) if use_graph else None
+        if bias is None and use_graph:
+            bias = self._dense_bias(x, q.dtype)
         if self._sdpa_ok and self.soft_cap is None:
             if bias is not None and is_causal:
                 sq, sk = q.shape[2], k.shape[2]

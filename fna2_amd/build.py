@@ -37,7 +37,7 @@ COMMON = [
 ]
 
 SOURCES = ["fna2_capi.cpp", "fna2_sched.hip", "fna2_fwd.hip", "fna2_bwd.hip", "fna2_bwd_dkdv.hip",
-           "fna2_bwd_dq.hip", "fna2_rope.hip"]
+           "fna2_bwd_dq.hip", "fna2_rope.hip", "fna2_decode.hip"]
 
 
 def _compile(src: Path, obj: Path, verbose: bool) -> None:

@@ -3,6 +3,7 @@
 // launch_* wrappers of the .hip files.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -604,6 +605,166 @@ int fna2_rope_bwd(const fna2_rope_bwd_args* b, void* stream) {
   P.dwq = P.wq ? b->dnorm_q : nullptr;
   P.dwk = P.wk ? b->dnorm_k : nullptr;
   if (fna2::launch_rope_norm_bwd(P, (hipStream_t)stream) != hipSuccess) return FNA2_E_LAUNCH;
+  return FNA2_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Work units of a decode launch are sized for MI355X's 256 compute units
+// (a fixed figure, so that the split count and the workspace size are a
+// function of the arguments alone).
+constexpr int kDecodeCUs = 256;
+constexpr int64_t kOff31 = ((int64_t)1 << 31) - 16;  // buffer-offset bound
+
+int dec_group(const fna2_decode_args& a) { return a.heads / a.heads_kv; }
+
+// Graph heads of the widest KV-head group and their rank chunks.
+int dec_graph_heads(const fna2_decode_args& a) {
+  return a.heads_graph > 0 ? std::min(dec_group(a), a.heads_graph) : 0;
+}
+int dec_rc(const fna2_decode_args& a) {
+  return fna2::decode_rank_chunks(dec_graph_heads(a) * (a.heads_graph > 0 ? a.rank / 8 : 0));
+}
+
+int check_bf16_rows(const fna2_tensor& t) {
+  if (!t.ptr) return FNA2_E_NULL;
+  if (!aligned(t.ptr, 16)) return FNA2_E_STRIDE;
+  if (t.stride_b < 0 || t.stride_s < 0 || t.stride_h < 0) return FNA2_E_STRIDE;
+  if (t.stride_b % 8 || t.stride_s % 8 || t.stride_h % 8) return FNA2_E_STRIDE;
+  return FNA2_OK;
+}
+
+struct DecSplit {
+  int n = 1, keys = 32;
+};
+
+DecSplit dec_split(const fna2_decode_args& a) {
+  DecSplit s;
+  const int64_t L = a.max_seqlen_k;
+  if (L <= 0) return s;
+  int64_t n = a.num_splits;
+  if (n <= 0) {
+    const int64_t units = std::max<int64_t>((int64_t)a.batch * a.heads_kv, 1);
+    const int rc = std::max(dec_rc(a), 0);
+    const int per_cu = std::max(1, (160 * 1024) / (fna2::kDecodeStages *
+                                                   fna2::decode_stage_bytes(a.head_dim, rc)));
+    const int64_t target = 2ll * kDecodeCUs * per_cu;  // two rounds of resident waves
+    n = std::min<int64_t>(cdiv64(target, units), cdiv64(L, 128));  // >= 4 steps a split
+    n = std::max<int64_t>(std::min<int64_t>(n, 64), 1);
+  }
+  n = std::min<int64_t>(n, cdiv64(L, 32));
+  s.keys = (int)(cdiv64(cdiv64(L, n), 32) * 32);
+  s.n = (int)cdiv64(L, s.keys);
+  return s;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fna2_check_decode(const fna2_decode_args* a) {
+  if (!a) return FNA2_E_NULL;
+  if (a->head_dim != 64 && a->head_dim != 128) return FNA2_E_HEAD_DIM;
+  if (a->heads <= 0 || a->heads_kv <= 0 || a->heads % a->heads_kv != 0) return FNA2_E_HEADS;
+  if (dec_group(*a) > 32) return FNA2_E_HEADS;
+  if (a->heads_graph < 0 || a->heads_graph > a->heads) return FNA2_E_HEADS;
+  const bool graph = a->heads_graph > 0;
+  if (graph && (a->rank < 8 || a->rank > 64 || a->rank % 8 != 0)) return FNA2_E_RANK;
+  if (graph && dec_rc(*a) < 0) return FNA2_E_RANK;
+  if (a->batch < 0 || a->max_seqlen_k < 0) return FNA2_E_SHAPE;
+  if (a->num_splits < 0 || a->num_splits > 64) return FNA2_E_SHAPE;
+  if (!std::isfinite(a->softmax_scale)) return FNA2_E_SCALE;
+  if (a->batch == 0) return FNA2_OK;
+  FNA2_TRY(check_bf16_rows(a->q));
+  FNA2_TRY(check_bf16_rows(a->out));
+  const bool rows = a->max_seqlen_k > 0;  // an empty cache is never read
+  if (rows) {
+    FNA2_TRY(check_bf16_rows(a->k_cache));
+    FNA2_TRY(check_bf16_rows(a->v_cache));
+  }
+  if (graph) {
+    FNA2_TRY(check_bf16_rows(a->r_q));
+    if (rows) FNA2_TRY(check_bf16_rows(a->rk_cache));
+    if (!a->graph_scale) return FNA2_E_NULL;
+  }
+  if (a->lse.ptr) {
+    if (!aligned(a->lse.ptr, 4) || a->lse.stride_b < 0 || a->lse.stride_h < 0)
+      return FNA2_E_STRIDE;
+  }
+  const int64_t g = dec_group(*a), D = a->head_dim;
+  if ((g - 1) * a->q.stride_h * 2 + D * 2 > kOff31) return FNA2_E_SHAPE;
+  if (32 * a->k_cache.stride_s * 2 > kOff31 || 32 * a->v_cache.stride_s * 2 > kOff31)
+    return FNA2_E_SHAPE;
+  if (graph) {
+    const int64_t gg = dec_graph_heads(*a), R = a->rank;
+    if ((gg - 1) * a->r_q.stride_h * 2 + R * 2 > kOff31) return FNA2_E_SHAPE;
+    if ((gg - 1) * a->rk_cache.stride_h * 2 + 31 * a->rk_cache.stride_s * 2 + R * 2 > kOff31)
+      return FNA2_E_SHAPE;
+  }
+  const DecSplit s = dec_split(*a);
+  if ((int64_t)a->batch * a->heads_kv * s.n > kMaxGrid) return FNA2_E_SHAPE;
+  return FNA2_OK;
+}
+
+int fna2_decode_num_splits(const fna2_decode_args* a) {
+  FNA2_TRY(fna2_check_decode(a));
+  return dec_split(*a).n;
+}
+
+size_t fna2_decode_workspace_bytes(const fna2_decode_args* a) {
+  if (fna2_check_decode(a) != FNA2_OK) return 0;
+  const DecSplit s = dec_split(*a);
+  if (s.n <= 1) return 0;
+  const size_t rows = (size_t)s.n * (size_t)a->batch * (size_t)a->heads;
+  return align_up(rows * (size_t)a->head_dim * 4u) + align_up(rows * 8u);
+}
+
+int fna2_decode(const fna2_decode_args* a, void* stream_ptr) {
+  FNA2_TRY(fna2_check_decode(a));
+  if (a->batch == 0) return FNA2_OK;
+  FNA2_TRY(check_device());
+  const DecSplit s = dec_split(*a);
+  const size_t need = fna2_decode_workspace_bytes(a);
+  if (need > 0 && (!a->workspace || a->workspace_bytes < need || !aligned(a->workspace, 16)))
+    return FNA2_E_WORKSPACE;
+  hipStream_t stream = (hipStream_t)stream_ptr;
+  fna2::DecodeParams K;
+  std::memset(&K, 0, sizeof(K));
+  K.B = a->batch;
+  K.H = a->heads;
+  K.H_KV = a->heads_kv;
+  K.H_G = a->heads_graph;
+  K.D = a->head_dim;
+  K.R = a->heads_graph > 0 ? a->rank : 0;
+  K.group = dec_group(*a);
+  K.nsplit = s.n;
+  K.split_keys = s.keys;
+  K.max_len = a->max_seqlen_k;
+  const float sc = a->softmax_scale;
+  K.c = sc > 0.f ? sc : sc < 0.f ? -sc : 1.f;
+  K.qa = sc > 0.f ? 1.f : sc < 0.f ? -1.f : 0.f;
+  K.c2 = K.c * fna2::kLog2e;
+  K.seqlens = a->seqlens_k;
+  K.q = view(a->q);
+  K.rq = view(a->r_q);
+  K.k = view(a->k_cache);
+  K.v = view(a->v_cache);
+  K.rk = view(a->rk_cache);
+  K.o = view(a->out);
+  K.lse = view(a->lse);
+  K.gs = a->graph_scale;
+  if (s.n > 1) {
+    const size_t rows = (size_t)s.n * (size_t)a->batch * (size_t)a->heads;
+    K.acc = (float*)a->workspace;
+    K.ml = (float*)((char*)a->workspace + align_up(rows * (size_t)a->head_dim * 4u));
+  }
+  const int rc = a->heads_graph > 0 ? dec_rc(*a) : 0;
+  if (!mark(a->events, 0, stream)) return FNA2_E_LAUNCH;
+  if (fna2::launch_decode(K, rc, stream) != hipSuccess) return FNA2_E_LAUNCH;
+  if (!mark(a->events, 1, stream)) return FNA2_E_LAUNCH;
+  if (fna2::launch_decode_merge(K, stream) != hipSuccess) return FNA2_E_LAUNCH;
   return FNA2_OK;
 }
 

@@ -75,6 +75,29 @@ int rope_blocks(int T);  // workgroups of a rotary launch over T tokens
 hipError_t launch_rope(const RopeParams& P, hipStream_t s);
 hipError_t launch_rope_norm_bwd(const RopeParams& P, hipStream_t s);
 
+// One-token decode against a KV cache (fna2_decode.hip).  q, rq, o, lse:
+// row (b, h) at ptr + b * sb + h * sh; caches: row j of (b, h) at
+// ptr + b * sb + h * sh + j * ss.
+struct DecodeParams {
+  int B, H, H_KV, H_G, D, R, group;
+  int nsplit;      // key splits per (sequence, KV head), <= 64
+  int split_keys;  // keys per split, a multiple of 32
+  int max_len;     // cache rows; lengths are clamped to it
+  float c, c2, qa;  // as in Problem
+  const int* seqlens;  // [B] valid rows per sequence, or null (all max_len)
+  TView q, rq, k, v, rk, o, lse;  // lse.ptr may be null
+  const float* gs;
+  float* acc;  // nsplit > 1: [nsplit][B][H][D] unnormalised numerators
+  float* ml;   // nsplit > 1: [nsplit][B][H] (max, sum) pairs
+};
+constexpr int kDecodeStages = 2;  // LDS ring depth of a decode wave
+// Rank-tile chunks of a decode kernel for `rch` used chunks (graph heads of
+// a group x R / 8): 0, 4, 8, 16 or 32; -1 if too wide.
+int decode_rank_chunks(int rch);
+int decode_stage_bytes(int D, int rc);
+hipError_t launch_decode(const DecodeParams& P, int rc, hipStream_t s);
+hipError_t launch_decode_merge(const DecodeParams& P, hipStream_t s);
+
 hipError_t launch_fwd(const FwdParams& P, int rp, int grid, hipStream_t s);
 hipError_t launch_bwd_dkdv(const BwdParams& P, int rpl, int grid, hipStream_t s);
 hipError_t launch_bwd_dq(const BwdParams& P, int rpl, int grid, hipStream_t s);

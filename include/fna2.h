@@ -197,6 +197,67 @@ int fna2_check_rope_bwd(const fna2_rope_bwd_args* args);
 /* Backward of fna2_rope_varlen (one launch without a norm, two with). */
 int fna2_rope_bwd(const fna2_rope_bwd_args* args, void* hip_stream);
 
+/* One-token decode against a KV cache.  Sequence b has one new query row per
+ * head and len_b cached rows (the new token's row included), all visible:
+ *     S_j = softmax_scale <q_h, K_j> + [h < H_G] graph_scale[h] <rq_h, Rk_hj>
+ * for j < len_b, normalised as in fna2_fwd (O = sum e^{S-m} V / (l + 1e-6)).
+ * The result equals the last row of the causal fna2_fwd over the sequence.
+ * With heads_graph = 0 it is the reference's decode step, which runs PyTorch
+ * SDPA over torch.cat(past_kv, new) (FNA2/attention_fna2.py:412-429,
+ * :445-473; no graph bias there because no Rk is cached).  Caching Rk
+ * (rk_cache) lets a model decode with the bias it was trained with.
+ *
+ * Layouts (element strides, feature stride 1, rows 16-byte aligned):
+ *   q   [B, H, D]          (b, h, f)    at ptr + b*stride_b + h*stride_h + f
+ *   r_q [B, H_G, R]        likewise; out [B, H, D] likewise (written)
+ *   k_cache, v_cache [B, H_KV, L, D]: (b, h, j, f) at
+ *                          ptr + b*stride_b + h*stride_h + j*stride_s + f
+ *   rk_cache [B, H_G, L, R] likewise
+ *   lse fp32 [B, H]        (b, h) at ptr + b*stride_b + h*stride_h
+ * H / H_KV may not exceed 32 (FNA2_E_HEADS: a group's heads are the 32
+ * columns of one MFMA tile), and the graph heads of one group times R may
+ * not exceed 256 (FNA2_E_RANK).  Byte offsets inside one (b, KV head) -- (H/H_KV - 1) *
+ * stride_h + 32 * stride_s of a cache, (H/H_KV - 1) * stride_h of q / r_q,
+ * in bytes -- must stay below 2^31 (FNA2_E_SHAPE). */
+typedef struct fna2_decode_args {
+  int32_t batch;        /* B >= 0                                           */
+  int32_t heads;        /* H                                                */
+  int32_t heads_kv;     /* H_KV: divides H                                  */
+  int32_t heads_graph;  /* H_G <= H (0: no bias; r_q, rk_cache unused)      */
+  int32_t head_dim;     /* D in {64, 128}                                   */
+  int32_t rank;         /* R: multiple of 8 in [8, 64] (if H_G > 0)         */
+  int32_t max_seqlen_k; /* L >= 0: rows each cache holds per (b, head)      */
+  int32_t num_splits;   /* key splits per (b, KV head): 0 = library's choice, else 1..64 */
+  float softmax_scale;
+  const int32_t* seqlens_k; /* [B] device int32 len_b (clamped to [0, L]); NULL: all L */
+  fna2_tensor q, r_q;
+  fna2_tensor k_cache, v_cache, rk_cache;
+  const float* graph_scale; /* [H_G] fp32 */
+  fna2_tensor out;          /* written                                      */
+  fna2_tensor lse;          /* written; ptr NULL: not computed              */
+  void* workspace;          /* fna2_decode_workspace_bytes                  */
+  size_t workspace_bytes;
+  /* Optional (may be NULL): FNA2_DECODE_EVENTS hipEvent_t handles, recorded
+   * around the split kernel. */
+  void* const* events;
+} fna2_decode_args;
+
+#define FNA2_DECODE_EVENTS 2
+
+/* Host-only validation of a decode call; no GPU call. */
+int fna2_check_decode(const fna2_decode_args* args);
+
+/* Key splits the call will use (num_splits, or the library's choice for the
+ * current device), or a negative status. */
+int fna2_decode_num_splits(const fna2_decode_args* args);
+
+/* Workspace bytes of a decode call (0 with one split). */
+size_t fna2_decode_workspace_bytes(const fna2_decode_args* args);
+
+/* Decode: one launch per split set, plus a merge launch with more than one
+ * split.  Writes out (and lse). */
+int fna2_decode(const fna2_decode_args* args, void* hip_stream);
+
 /* ABI version (FNA2_ABI_VERSION). */
 int fna2_version(void);
 

@@ -31,6 +31,10 @@ Layouts follow the reference API: dense q ``[B,H,S,D]``, k/v ``[B,H_KV,S,D]``,
 r ``[B,H_G,S,R]``, lse ``[B,H,S]``; varlen q ``[T,H,D]``, lse ``[T,H]`` with
 ``cu_seqlens`` int32 offsets.
 
+* Decode (``decode``): one query row per sequence against the first len_b
+  rows of a KV cache, all visible -- the reference's decode step with the
+  graph bias kept when an Rk cache is given (attention_fna2.py:412-429).
+
 Pinning (tests/test_oracle.py): a pure-Python brute force on tiny inputs,
 torch's ``scaled_dot_product_attention`` (``is_causal=True`` with gs = 0, an
 explicit float mask otherwise), torch autograd of that library forward at
@@ -214,6 +218,41 @@ def backward(dout, q, k, v, rq, rk, gs, out, lse, scale, causal=True, cu_q=None,
             drk[irk] += dRk
             dgs[h] += dg
     return dq, dk, dv, drq, drk, dgs
+
+
+def decode(q, k_cache, v_cache, rq, rk_cache, gs, scale, seqlens=None, dtype=np.float64,
+           eps=EPS):
+    """One-token decode against a KV cache: for sequence b and head h, the
+    query row q[b, h] attends to the first ``seqlens[b]`` cache rows (all of
+    them visible), with the graph bias for h < H_G.  q ``[B, H, D]``, caches
+    ``[B, H_KV, L, D]``, rq ``[B, H_G, R]``, rk_cache ``[B, H_G, L, R]``.
+    Returns (out ``[B, H, D]``, lse ``[B, H]``).
+
+    This is the non-causal ``head_forward`` on one row, i.e. the last row of
+    the causal forward over the sequence (the identity the tests pin), and
+    for H_G = 0 the reference's decode step, SDPA over
+    ``torch.cat(past_kv, new)`` (FNA2/attention_fna2.py:412-429, :445-473).
+    """
+    q, kc, vc = _as(q, dtype), _as(k_cache, dtype), _as(v_cache, dtype)
+    rq, rkc, gs = _as(rq, dtype), _as(rk_cache, dtype), _as(gs, dtype)
+    B, H, D = q.shape
+    H_KV, L = kc.shape[1], kc.shape[2]
+    H_G = 0 if rq is None else rq.shape[1]
+    G = H // H_KV
+    lens = np.full(B, L, dtype=np.int64) if seqlens is None else \
+        np.clip(_as(seqlens, np.int64), 0, L)
+    out = np.zeros((B, H, D), dtype=dtype)
+    lse = np.full((B, H), -np.inf, dtype=dtype)
+    for b in range(B):
+        n = int(lens[b])
+        for h in range(H):
+            g = h < H_G
+            o, l = head_forward(q[b, h][None], kc[b, h // G, :n], vc[b, h // G, :n],
+                                rq[b, h][None] if g else None, rkc[b, h, :n] if g else None,
+                                gs[h] if g else 0.0, scale, False, eps)
+            out[b, h] = o[0]
+            lse[b, h] = l[0]
+    return out, lse
 
 
 def flops(cu_or_lengths, H, D, R, causal, H_G=None):

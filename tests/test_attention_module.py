@@ -31,7 +31,8 @@ def _params(fn):
 
 
 def test_signatures_match_reference():
-    assert _params(A.NaylisAttention.__init__) == CTOR
+    # the reference's parameters, in order, then one extra keyword
+    assert _params(A.NaylisAttention.__init__) == CTOR + [("decode_graph_bias", False)]
     assert _params(A.NaylisAttention.forward) == FWD
     assert A._FNA2_BLOCK_R == 32
 
@@ -62,6 +63,32 @@ def test_eager_path_on_cpu_is_causal_attention():
     x2[:, 5:] += 1.0
     y2, _ = m(x2)
     torch.testing.assert_close(y[:, :5], y2[:, :5], atol=1e-5, rtol=1e-5)
+
+
+def test_decode_graph_bias_cache_and_eager_decode():
+    """decode_graph_bias: the cache is (k, v, r_k) and a decode step equals
+    the full causal forward's last row (eager backends, CPU)."""
+    torch.manual_seed(2)
+    m = A.NaylisAttention(128, 4, n_kv_heads=2, rel_rank=8, vanilla_heads=1, use_fna2=False,
+                          decode_graph_bias=True).eval()
+    with torch.no_grad():
+        m.graph_scale.fill_(2.0)
+    x = torch.randn(2, 9, 128)
+    with torch.no_grad():
+        y_full, _ = m(x)
+        _, cache = m(x[:, :8], use_kv_cache=True)
+        assert len(cache) == 3 and cache[2].shape == (2, 3, 8, 8)
+        y_step, cache2 = m(x[:, 8:], past_kv=cache, use_kv_cache=True)
+    assert cache2[0].shape[2] == 9 and cache2[2].shape[2] == 9
+    assert (y_step[:, 0] - y_full[:, 8]).abs().max().item() < 2e-2
+    # without the bias (the reference's decode) the step differs
+    plain = copy.deepcopy(m)
+    plain.decode_graph_bias = False
+    with torch.no_grad():
+        y_plain, _ = plain(x[:, 8:], past_kv=cache[:2])
+    assert (y_plain[:, 0] - y_full[:, 8]).abs().max().item() > 1e-2
+    with pytest.raises(ValueError):
+        m(x[:, 8:], past_kv=cache[:2])
 
 
 # ── GPU: the FNA2 path against the module's own eager path ──────────────────
@@ -136,3 +163,29 @@ def test_fused_projection_equals_separate_projections(lead):
         torch.testing.assert_close(got.float(), want.to(torch.bfloat16).float(), atol=1e-2, rtol=0)
     # q, k, v are views of one buffer (no copies)
     assert q.untyped_storage().data_ptr() == k.untyped_storage().data_ptr() == v.untyped_storage().data_ptr()
+
+
+@pytest.mark.gpu
+def test_kernel_decode_step_matches_full_forward_and_reference_decode(gpu):
+    """Decoding one token against the cache on the kernel: with
+    decode_graph_bias it equals the FNA2 forward's last row; without, the
+    reference's decode step (eager SDPA over the cache, no bias; CPU)."""
+    ref, fast = _pair(embed_dim=512, num_heads=8, n_kv_heads=2, rel_rank=32, vanilla_heads=2)
+    ref.eval()
+    fast.eval()
+    x = torch.randn(2, 70, 512)
+    xc = x.cuda()
+    with torch.no_grad():
+        _, cache = fast(xc[:, :69], use_kv_cache=True)
+        y_step, _ = fast(xc[:, 69:], past_kv=cache)
+        _, rcache = ref(x[:, :69], use_kv_cache=True)
+        y_ref, _ = ref(x[:, 69:], past_kv=rcache)
+    assert (y_step.cpu() - y_ref).abs().max().item() < 2e-2
+    biased = copy.deepcopy(fast)
+    biased.decode_graph_bias = True
+    with torch.no_grad():
+        y_full, _ = biased(xc)
+        _, bcache = biased(xc[:, :69], use_kv_cache=True)
+        assert len(bcache) == 3
+        y_bstep, _ = biased(xc[:, 69:], past_kv=bcache)
+    assert (y_bstep[:, 0] - y_full[:, 69]).abs().max().item() < 2e-2

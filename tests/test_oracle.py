@@ -307,3 +307,78 @@ def test_planted_mistakes_are_caught(monkeypatch, mutation):
         monkeypatch.setattr(O, "head_forward", bad_fwd)
     with pytest.raises(AssertionError):
         _run_pins()
+
+
+# ── decode (one query row against a KV cache) ─────────────────────────────────
+
+def _decode_case(seed, B=3, H=6, HKV=2, HG=4, D=8, R=4, L=11):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((B, H, L, D))
+    k = rng.standard_normal((B, HKV, L, D))
+    v = rng.standard_normal((B, HKV, L, D))
+    rq = rng.standard_normal((B, HG, L, R))
+    rk = rng.standard_normal((B, HG, L, R))
+    gs = rng.standard_normal(HG)
+    lens = np.array([L, 1, 7][:B])
+    return q, k, v, rq, rk, gs, lens
+
+
+def test_decode_is_last_row_of_causal_forward():
+    """Row len-1 of the causal forward over the sequence (the causal mask
+    path) equals the decode of that row against the first len cache rows (the
+    truncation path)."""
+    q, k, v, rq, rk, gs, lens = _decode_case(11)
+    B, H = q.shape[:2]
+    scale = 0.37
+    qd = np.stack([q[b, :, lens[b] - 1] for b in range(B)])
+    rqd = np.stack([rq[b, :, lens[b] - 1] for b in range(B)])
+    out, lse = O.decode(qd, k, v, rqd, rk, gs, scale, seqlens=lens)
+    for b in range(B):
+        n = lens[b]
+        of, lf = O.forward(q[b:b + 1, :, :n], k[b:b + 1, :, :n], v[b:b + 1, :, :n],
+                           rq[b:b + 1, :, :n], rk[b:b + 1, :, :n], gs, scale, causal=True)
+        np.testing.assert_allclose(out[b], of[0, :, n - 1], rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(lse[b], lf[0, :, n - 1], rtol=1e-12, atol=1e-12)
+
+
+def test_decode_without_bias_is_torch_sdpa_over_the_cache():
+    """H_G = 0: the reference's decode step, SDPA (no mask) over the cached
+    rows with the KV heads repeated per group."""
+    q, k, v, _, _, _, lens = _decode_case(12)
+    B, H = q.shape[:2]
+    G = H // k.shape[1]
+    qd = q[:, :, 0]
+    out, _ = O.decode(qd, k, v, None, None, None, 0.5, seqlens=lens)
+    for b in range(B):
+        n = lens[b]
+        kt = torch.from_numpy(k[b:b + 1, :, :n]).repeat_interleave(G, dim=1)
+        vt = torch.from_numpy(v[b:b + 1, :, :n]).repeat_interleave(G, dim=1)
+        ref = F.scaled_dot_product_attention(torch.from_numpy(qd[b:b + 1, :, None]), kt, vt,
+                                             scale=0.5)
+        np.testing.assert_allclose(out[b], ref[0, :, 0].numpy(), rtol=0, atol=1e-5)
+
+
+def test_decode_empty_cache_rows():
+    q, k, v, rq, rk, gs, _ = _decode_case(13)
+    out, lse = O.decode(q[:, :, 0], k, v, rq[:, :, 0], rk, gs, 0.5, seqlens=np.array([0, 0, 0]))
+    assert np.all(out == 0) and np.all(np.isneginf(lse))
+
+
+@pytest.mark.parametrize("mutation", ["len_off_by_one", "bias_on_kv_head_rk"])
+def test_decode_planted_mistakes_are_caught(monkeypatch, mutation):
+    orig = O.head_forward
+    if mutation == "len_off_by_one":
+        def bad(Q, K, V, Rq, Rk, g, scale, causal, eps=O.EPS):
+            if K.shape[0] > 1 and not causal:
+                K, V = K[:-1], V[:-1]
+                Rk = None if Rk is None else Rk[:-1]
+            return orig(Q, K, V, Rq, Rk, g, scale, causal, eps)
+    else:
+        def bad(Q, K, V, Rq, Rk, g, scale, causal, eps=O.EPS):
+            if Rk is not None and not causal:
+                Rk = Rk[::-1]
+            return orig(Q, K, V, Rq, Rk, g, scale, causal, eps)
+    monkeypatch.setattr(O, "head_forward", bad)
+    with pytest.raises(AssertionError):
+        test_decode_is_last_row_of_causal_forward()
+        test_decode_without_bias_is_torch_sdpa_over_the_cache()
