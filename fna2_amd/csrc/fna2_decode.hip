@@ -56,7 +56,7 @@ struct DecCfg {
   // VMEM instructions per step (a constant: the ring waits are immediates)
   static constexpr int OPS = 2 * (CD / 2) + NRK;
   static_assert(RC % 4 == 0, "rank chunks come in column groups of 4");
-  static_assert(NS >= 2 && (NS - 2) * OPS < 64, "ring wait out of vmcnt range");
+  static_assert(NS >= 2 && NS <= 4 && (NS - 2) * OPS < 64, "ring depth");
 };
 
 // Wait until at most N of this wave's vector-memory operations are in flight
@@ -77,6 +77,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& P) {
   __shared__ __attribute__((aligned(1024))) uint8_t st0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t st1[C::STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t st2[NS > 2 ? C::STAGE : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t st3[NS > 3 ? C::STAGE : 16];
   const int lane = threadIdx.x;
   const int col = lane & 31, hl = lane >> 5;  // head column in the group; k half
   const int u = blockIdx.x;
@@ -136,7 +137,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& P) {
   };
   auto stage = [&](auto si) -> uint8_t* {
     constexpr int s = decltype(si)::value;
-    return s == 0 ? st0 : s == 1 ? st1 : st2;
+    return s == 0 ? st0 : s == 1 ? st1 : s == 2 ? st2 : st3;
   };
 
   // The first NS - 1 tiles go out before the query loads, so the latencies
