@@ -66,9 +66,10 @@ def parse():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy (the known-size kernel that "
                          "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE) and print its rate")
-    ap.add_argument("--summarize-pmc", nargs=2, metavar=("WORKLOAD_DIR", "COPY_DIR"),
-                    help="turn rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this bench and "
-                         "of --copy-calibration into profiles/traffic_<config>.json")
+    ap.add_argument("--summarize-pmc", nargs="+", metavar="DIR",
+                    help="WORKLOAD_DIR COPY_DIR [NAME]: turn rocprofv3 --pmc FETCH_SIZE / "
+                         "WRITE_SIZE runs of this bench and of --copy-calibration into "
+                         "profiles/traffic_<NAME>.json (NAME defaults to --config)")
     ap.add_argument("--summarize-trace", nargs=3, metavar=("DB_DIR", "OUT_MD", "COMMAND"),
                     help="write the rocprofv3 --kernel-trace --stats table of DB_DIR to OUT_MD")
     ap.add_argument("--summarize-counters", nargs=3, metavar=("DB_DIR", "OUT_MD", "COMMAND"),
@@ -188,7 +189,7 @@ def summarize_pmc(work_dir, copy_dir, config):
 
 def measured_traffic(config, kernel):
     """HBM bytes per launch of `kernel` from profiles/traffic_<config>.json, or None."""
-    key = {"fwd": "fwd_kernel", "dkdv": "dkdv_kernel", "dq": "dq_kernel"}[kernel]
+    key = {"fwd": "fwd_kernel", "dkdv": "dkdv_kernel", "dq": "dq_kernel"}.get(kernel, kernel)
     try:
         with open(os.path.join(TRAFFIC_DIR, f"traffic_{config}.json")) as fh:
             ks = json.load(fh)["kernels"]
@@ -606,7 +607,10 @@ def decode_bench(args):
                                "heads, R=32), 16 KV heads, d=128 (c3's attention geometry)",
                    "num_splits": r["splits"]},
         "roofline": {"bound": "hbm", "achieved": round(kgbs, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(kgbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(kgbs / PEAK_HBM_GBS, 4),
+                     "traffic": measured_traffic("decode", "decode_kernel_d128_c4"),
+                     "traffic_source": "profiles/traffic_decode.json (rocprofv3 FETCH_SIZE + "
+                                       "WRITE_SIZE per dispatch, copy-calibrated)",
                      "kernel": "decode_kernel_d128_c4", "algorithmic_bytes": r["bytes"],
                      "kernel_ms": round(r["kernel_ms"], 5)},
         "eager_reference_ms": {"with_bias": round(r["eager_ms"], 4),
@@ -656,7 +660,10 @@ def main():
         copy_calibration()
         return
     if args.summarize_pmc:
-        summarize_pmc(*args.summarize_pmc, args.config)
+        if len(args.summarize_pmc) not in (2, 3):
+            sys.exit("--summarize-pmc takes WORKLOAD_DIR COPY_DIR [NAME]")
+        summarize_pmc(*args.summarize_pmc[:2],
+                      args.summarize_pmc[2] if len(args.summarize_pmc) == 3 else args.config)
         return
     if args.summarize_trace:
         summarize_trace(*args.summarize_trace)
