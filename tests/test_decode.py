@@ -121,6 +121,12 @@ CASES = [
     (1, 32, 1, 8, 64, 8, 150, [150]),            # group 32
     (2, 8, 1, 8, 128, 32, 96, [96, 95]),         # 8 graph heads x 32 = widest rank tile
     (2, 4, 2, 4, 128, 64, 64, [0, 64]),          # an empty cache
+    # the remaining kernel instances (head dim x rank-tile chunks)
+    (2, 8, 8, 8, 128, 32, 90, [90, 45]),         # d128, 4 rank chunks
+    (2, 8, 4, 8, 128, 32, 90, [90, 3]),          # d128, 8 rank chunks
+    (2, 8, 2, 0, 64, 0, 90, [90, 60]),           # d64, no graph heads
+    (2, 8, 2, 8, 64, 32, 90, [90, 61]),          # d64, 16 rank chunks
+    (2, 8, 2, 8, 64, 64, 90, [90, 33]),          # d64, 32 rank chunks
 ]
 
 
