@@ -309,7 +309,12 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     };
 
     // S and dP of this wave's 32 keys against block qi of the cursor.
-    auto scores = [&](const KvCursor& c, const uint8_t* cur, f32x16& sacc, f32x16& dpacc) {
+    // The block's -LSE log2(e) and delta rows go to lsr (this lane's query
+    // rows 8 gq + 4 hl .. +3, gq = 0..3: -LSE in lsr[gq], delta in
+    // lsr[4 + gq]), read with the operands so their latency hides under the
+    // MFMAs.
+    auto scores = [&](const KvCursor& c, const uint8_t* cur, f32x16& sacc, f32x16& dpacc,
+                      f32x4_t (&lsr)[8]) {
       // (A vanilla head, or rank padding, has zero rank operands: its rank
       // MFMAs add exact zeros and keep the block one basic block.)
       const uint8_t* qt = cur;
@@ -324,6 +329,12 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       for (int s = 0; s < C::KSR; ++s) qa[C::KSD + s] = row_read<C::BM>(rt, rdl, 0, s);
 #pragma unroll
       for (int s = 0; s < C::KSD; ++s) oa[s] = row_read<C::BM>(ot, rdl, 0, s);
+      const float* ls = (const float*)(cur + C::QB + C::RB + C::OB);
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        lsr[gq] = *(const f32x4_t*)(ls + 8 * gq + 4 * hl);
+        lsr[4 + gq] = *(const f32x4_t*)(ls + 64 + 8 * gq + 4 * hl);
+      }
       sacc = f32x16{};
       dpacc = f32x16{};
 #pragma unroll
@@ -334,48 +345,58 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
 #pragma unroll
       for (int s = 0; s < C::KSR; ++s) sacc = mfma32(qa[C::KSD + s], as_bf16x8(kreg[C::KSD + s]), sacc);
       // issue order: every read, then every MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 2 * C::KSD + C::KSR, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * C::KSD + C::KSR + 8, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 2 * C::KSD + C::KSR, 0);
     };
     // P = exp(S - LSE) and dS = P (dP - delta) to LDS in the B-operand layout
     // of the consumer's MFMAs: for k-half j (query rows 16j..16j+15), lane
     // (key l32, half hl) holds rows 16j + 8i + 4hl + e, i = 0..1, e = 0..3,
     // i.e. accumulator registers 8j..8j+7.
-    auto softmax = [&](const KvCursor& c, const uint8_t* cur, uint8_t* pd, const f32x16& sacc,
-                       const f32x16& dpacc) {
+    auto softmax = [&](const KvCursor& c, uint8_t* pd, const f32x16& sacc,
+                       const f32x16& dpacc, const f32x4_t (&lsr)[8]) {
       const KvItem& x = c.it;
       const int qbase = (x.qb_lo + c.qi) * C::BM;
-      const float* ls = (const float*)(cur + C::QB + C::RB + C::OB);
       // Zero-filled query rows (past the sequence) have Q = dO = LSE =
       // delta = 0, so P (dP - delta) = 0 there; columns of keys past the
       // sequence are never stored.  Only the causal diagonal needs a mask:
-      // query row qbase + r sees key k0t + krow iff r >= thr.
-      const int thr = (p.causal && x.k0t + kw * 32 + 31 > qbase) ? x.k0t + krow - qbase
-                                                                  : -(1 << 30);
-      u32x4 pk[2], dk[2];
+      // query row qbase + r sees key k0t + krow iff r >= thr.  Blocks off
+      // the diagonal (every block of a non-causal problem) skip the compare
+      // and select, a fifth of the arithmetic per score.
+      const bool diag = p.causal && x.k0t + kw * 32 + 31 > qbase;  // wave-uniform
+      const int thr = x.k0t + krow - qbase;
+      auto body = [&](auto masked) {
+        u32x4 pk[2], dk[2];
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const int r0 = 8 * gq + 4 * hl;
-        const f32x4_t nl4 = *(const f32x4_t*)(ls + r0);
-        const f32x4_t dl4 = *(const f32x4_t*)(ls + 64 + r0);
-        float pv[4], dv[4];
+        for (int gq = 0; gq < 4; ++gq) {
+          const int r0 = 8 * gq + 4 * hl;
+          const f32x4_t nl4 = lsr[gq];
+          const f32x4_t dl4 = lsr[4 + gq];
+          float pv[4], dv[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int v = 4 * gq + j;
-          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[v], p.c2, nl4[j]));
-          pv[j] = r0 + j >= thr ? e : 0.f;
-          dv[j] = pv[j] * (dpacc[v] - dl4[j]);
+          for (int j = 0; j < 4; ++j) {
+            const int v = 4 * gq + j;
+            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[v], p.c2, nl4[j]));
+            if constexpr (decltype(masked)::value)
+              pv[j] = r0 + j >= thr ? e : 0.f;
+            else
+              pv[j] = e;
+            dv[j] = pv[j] * (dpacc[v] - dl4[j]);
+          }
+          pk[gq >> 1][2 * (gq & 1)] = pack_bf16(pv[0], pv[1]);
+          pk[gq >> 1][2 * (gq & 1) + 1] = pack_bf16(pv[2], pv[3]);
+          dk[gq >> 1][2 * (gq & 1)] = pack_bf16(dv[0], dv[1]);
+          dk[gq >> 1][2 * (gq & 1) + 1] = pack_bf16(dv[2], dv[3]);
         }
-        pk[gq >> 1][2 * (gq & 1)] = pack_bf16(pv[0], pv[1]);
-        pk[gq >> 1][2 * (gq & 1) + 1] = pack_bf16(pv[2], pv[3]);
-        dk[gq >> 1][2 * (gq & 1)] = pack_bf16(dv[0], dv[1]);
-        dk[gq >> 1][2 * (gq & 1) + 1] = pack_bf16(dv[2], dv[3]);
-      }
-      uint8_t* o = pd + kw * C::PW + lane * 16;
-      st16(o, pk[0]);
-      st16(o + 1024, pk[1]);
-      st16(o + 2048, dk[0]);
-      st16(o + 3072, dk[1]);
+        uint8_t* o = pd + kw * C::PW + lane * 16;
+        st16(o, pk[0]);
+        st16(o + 1024, pk[1]);
+        st16(o + 2048, dk[0]);
+        st16(o + 3072, dk[1]);
+      };
+      if (diag)
+        body(std::true_type{});
+      else
+        body(std::false_type{});
     };
 
     // The ring: every step issues exactly C::NB VMEM instructions (the DMA
@@ -403,7 +424,9 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
 
     // Block T (stage `cur`): wait for its tiles; S, dP; at the last block of
     // an (item, head), load the next one's rows into the registers just
-    // read; start the DMA of block T + 2; P, dS.
+    // read; P, dS; start the DMA of block T + 2.  (P and dS go before the
+    // DMA: the DMA's issue can stall on the memory pipeline, and the
+    // consumers wait for P and dS.)
     auto step = [&](const uint8_t* cur, uint8_t* nxt, uint8_t* pd) {
       ring_barrier<C::NB>();
       if (pc.done) return;
@@ -415,18 +438,19 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       advance(nx, no_zero);
       const bool act = block_active(pc);
       f32x16 sacc, dpacc;
+      f32x4_t lsr[8];
       __builtin_amdgcn_sched_barrier(0);
-      if (act) scores(pc, cur, sacc, dpacc);
+      if (act) scores(pc, cur, sacc, dpacc, lsr);
       __builtin_amdgcn_sched_barrier(0);
       if (!nx.done && nx.qi == 0) load_rows(nx.it, nx.it.kvh * p.group + nx.hi);
+      __builtin_amdgcn_sched_barrier(0);
+      if (act) softmax(pc, pd, sacc, dpacc, lsr);
       __builtin_amdgcn_sched_barrier(0);
       issue(ic, nxt);
       if (!ic.done) {
         advance(ic, no_zero);
         if (ic.done || ic.qi == 0) setup(ic);
       }
-      __builtin_amdgcn_sched_barrier(0);
-      if (act) softmax(pc, cur, pd, sacc, dpacc);
       __builtin_amdgcn_sched_barrier(0);
       pc = nx;
     };
