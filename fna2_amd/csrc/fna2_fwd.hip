@@ -191,10 +191,21 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sacc[kb2][v]);
     mx = wave_pair_max(mx);
-    const float m_new = fmaxf(m_i, mx);
-    const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f((m_i - m_use) * p.c2);
-    const float nm = -m_use * p.c2;
+    // Lazy rescale: the running maximum m_i moves (and O, l are rescaled)
+    // only when some query's maximum has grown by more than 8 in exp2 units.
+    // Otherwise the stale m_i stays: P <= 2^8, which bf16 and fp32 hold with
+    // the same relative precision, and O / l and the LSE come out the same
+    // (up to the 1e-6 of the normaliser).  Past the first key tile the
+    // rescale is then rare.
+    if (__builtin_amdgcn_ballot_w64((mx - m_i) * p.c2 > 8.f) != 0) {
+      const float m_new = fmaxf(m_i, mx);
+      const float alpha = __builtin_amdgcn_exp2f((m_i - ((m_new == kNegInf) ? 0.f : m_new)) * p.c2);
+      l_i *= alpha;
+#pragma unroll
+      for (int d = 0; d < D / 32; ++d) oacc[d] *= alpha;
+      m_i = m_new;
+    }
+    const float nm = -((m_i == kNegInf) ? 0.f : m_i) * p.c2;
     float ls = 0.f;
     bf16x8 pb[C::BN / 16];
 #pragma unroll
@@ -212,10 +223,7 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
         }
         pb[kb2 * 2 + half] = as_bf16x8(pk);
       }
-    l_i = l_i * alpha + ls;
-    m_i = m_new;
-#pragma unroll
-    for (int d = 0; d < D / 32; ++d) oacc[d] *= alpha;
+    l_i += ls;
     // O^T += V^T P^T
 #pragma unroll
     for (int s = 0; s < C::BN / 16; ++s)
