@@ -3,8 +3,11 @@
 The hot path is ``flash_naylis_attn`` (module ``flash_naylis_attn``), backed by
 hand-written HIP kernels in ``csrc/`` behind the C ABI of ``include/fna2.h``.
 ``attention_fna2`` holds the ``NaylisAttention`` caller with the reference's
-constructor and forward signatures.
+constructor and forward signatures.  Around the path: ``rope.rope_varlen``
+(varlen rotary embedding, optionally with the QK RMSNorm) and
+``decode.flash_naylis_decode`` (one-token decode against a KV cache).
 """
+from .decode import flash_naylis_decode  # noqa: F401
 from .flash_naylis_attn import (  # noqa: F401
     BLOCK_M,
     BLOCK_N,
@@ -12,5 +15,7 @@ from .flash_naylis_attn import (  # noqa: F401
     FlashNaylisAttnFunc,
     flash_naylis_attn,
 )
+from .rope import rope_varlen  # noqa: F401
 
-__all__ = ["BLOCK_M", "BLOCK_N", "BLOCK_R", "FlashNaylisAttnFunc", "flash_naylis_attn"]
+__all__ = ["BLOCK_M", "BLOCK_N", "BLOCK_R", "FlashNaylisAttnFunc", "flash_naylis_attn",
+           "flash_naylis_decode", "rope_varlen"]
