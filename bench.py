@@ -590,11 +590,66 @@ def decode_bench(args):
                     splits=lib.fna2_decode_num_splits(ctypes.byref(a)),
                     inputs=(q, k, v, rq, rk, gs, scale))
 
+    def module_steps(steps):
+        """One NaylisAttention decode step (E = 2048, 16 heads of 128, all
+        graph heads, rank 32; bf16) for 64 sequences against 4095 cached
+        rows: the reference's pattern (tuple cache grown by torch.cat, SDPA
+        without the bias: the module built with use_fna2=False), the tuple
+        cache on the decode kernel, and a StaticKVCache (written in place),
+        with and without the bias."""
+        from fna2_amd import attention_fna2 as A
+        B, L, E = 64, 4095, 2048
+        torch.manual_seed(0)
+        res = {}
+        x = torch.randn(B, 1, E, device=dev, dtype=torch.bfloat16)
+        for name, fna2, bias, static in (("reference_eager", False, False, False),
+                                         ("tuple_cache", True, False, False),
+                                         ("static_cache", True, False, True),
+                                         ("static_cache_bias", True, True, True)):
+            m = A.NaylisAttention(E, 16, rel_rank=32, use_fna2=fna2,
+                                  decode_graph_bias=bias).to(dev).to(torch.bfloat16).eval()
+            if fna2 and not m._use_fna2:
+                raise RuntimeError("decode bench: the FNA2 kernels are not available")
+            g = torch.Generator(device=dev).manual_seed(1)
+            rows = [torch.randn(B, 16, L, 128, device=dev, dtype=torch.bfloat16, generator=g)
+                    for _ in range(2)]
+            if bias:
+                rows.append(torch.randn(B, 16, L, 32, device=dev, dtype=torch.bfloat16,
+                                        generator=g) * 32 ** -0.5)
+            if static:
+                cache = A.StaticKVCache.empty(B, 16, L + steps + 8, 128, 16 if bias else 0, 32,
+                                              device=dev)
+                cache.append(*rows)
+                step = lambda: m(x, past_kv=cache, use_kv_cache=True)
+                reset = lambda: setattr(cache, "length", L)
+            else:
+                past = tuple(rows)
+                step = lambda: m(x, past_kv=past, use_kv_cache=True)
+                reset = lambda: None
+            with torch.no_grad():
+                for _ in range(3):
+                    step()
+                    reset()
+                torch.cuda.synchronize()
+                ts = []
+                for _ in range(steps):
+                    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    a.record()
+                    step()
+                    b.record()
+                    torch.cuda.synchronize()
+                    reset()
+                    ts.append(a.elapsed_time(b))
+            res[name] = round(statistics.median(ts), 4)
+            del m, rows
+        return res
+
     main_shape = (64, 16, 16, 16, 128, 32, 4096)
     gqa_shape = (64, 32, 8, 32, 128, 32, 4096)
     r = measure(main_shape, True, args.steps, args.warmup)
     r0 = measure(main_shape, False, args.steps, args.warmup)
     rg = measure(gqa_shape, True, args.steps, args.warmup)
+    mod = module_steps(max(args.steps // 5, 5))
     gbs = r["bytes"] / (r["ms"] * 1e-3) / 1e9
     kgbs = r["bytes"] / (r["kernel_ms"] * 1e-3) / 1e9
     line = {
@@ -619,6 +674,7 @@ def decode_bench(args):
         "without_bias": {"ms": round(r0["ms"], 5),
                          "GBps": round(r0["bytes"] / (r0["ms"] * 1e-3) / 1e9, 1),
                          "speedup_over_reference_sdpa": round(r0["eager_ms"] / r0["ms"], 2)},
+        "module_step_ms": mod,
         "gqa_32q_8kv": {"ms": round(rg["ms"], 5), "kernel_ms": round(rg["kernel_ms"], 5),
                         "GBps": round(rg["bytes"] / (rg["ms"] * 1e-3) / 1e9, 1),
                         "kernel_GBps": round(rg["bytes"] / (rg["kernel_ms"] * 1e-3) / 1e9, 1),

@@ -13,7 +13,9 @@ The module keeps the reference's constructor and ``forward`` signatures
   ``torch.cat(past_kv, new)`` (:412-429, :445-473): the same result, without
   the graph bias, as there.  ``decode_graph_bias=True`` (an extra keyword)
   keeps ``R_k`` in the cache, ``(k, v, r_k)``, and decodes with the bias, so
-  that a decode step equals the last row of the full causal forward;
+  that a decode step equals the last row of the full causal forward.
+  ``past_kv`` may also be a ``StaticKVCache`` (preallocated, written in
+  place: no per-step copy of the cache);
 * the other paths the reference sends elsewhere keep going elsewhere:
   ``soft_cap`` and modules built with ``use_fna2=False`` use PyTorch's SDPA
   with a materialised bias, or the explicit softmax when a ``soft_cap`` or
@@ -64,6 +66,61 @@ _flash_naylis_attn = flash_naylis_attn
 KVCache = Tuple[torch.Tensor, ...]
 
 
+class StaticKVCache:
+    """A preallocated KV cache, written in place (an alternative to the
+    reference's tuple cache, which ``torch.cat`` grows by a full copy per
+    step: attention_fna2.py:415-418).
+
+    ``k``, ``v``: ``[B, H_KV, capacity, D]``; ``r_k``: ``[B, H_G, capacity,
+    R]`` for modules built with ``decode_graph_bias=True``.  ``length`` rows
+    are in use, the same for every sequence.  Pass it as ``past_kv``: the
+    module appends the new rows and attends to the first ``length`` (the
+    decode kernel reads them in place), and returns the same object."""
+
+    def __init__(self, k: torch.Tensor, v: torch.Tensor, r_k: Optional[torch.Tensor] = None,
+                 length: int = 0):
+        assert k.shape == v.shape and k.dim() == 4, "k and v must be [B, H_KV, capacity, D]"
+        assert r_k is None or (r_k.dim() == 4 and r_k.shape[:3] == (k.shape[0], r_k.shape[1],
+                                                                     k.shape[2]))
+        assert 0 <= length <= k.shape[2]
+        self.k, self.v, self.r_k, self.length = k, v, r_k, int(length)
+
+    @classmethod
+    def empty(cls, batch: int, n_kv_heads: int, capacity: int, head_dim: int,
+              graph_heads: int = 0, rank: int = 0, dtype=torch.bfloat16,
+              device=None) -> "StaticKVCache":
+        mk = lambda h, f: torch.zeros(batch, h, capacity, f, dtype=dtype, device=device)
+        return cls(mk(n_kv_heads, head_dim), mk(n_kv_heads, head_dim),
+                   mk(graph_heads, rank) if graph_heads > 0 else None)
+
+    @property
+    def capacity(self) -> int:
+        return self.k.shape[2]
+
+    def append(self, k: torch.Tensor, v: torch.Tensor, r_k: Optional[torch.Tensor] = None):
+        """Write rows [length, length + S) from k, v ``[B, H_KV, S, D]`` (and
+        r_k ``[B, H_G, S, R]``)."""
+        s = k.shape[2]
+        if self.length + s > self.capacity:
+            raise ValueError(f"StaticKVCache full: {self.length} + {s} rows > capacity "
+                             f"{self.capacity}")
+        end = self.length + s
+        self.k[:, :, self.length:end] = k
+        self.v[:, :, self.length:end] = v
+        if self.r_k is not None:
+            if r_k is None:
+                raise ValueError("this cache holds R_k: the module must keep it "
+                                 "(decode_graph_bias=True)")
+            self.r_k[:, :, self.length:end] = r_k
+        self.length = end
+
+    def view(self) -> KVCache:
+        """The rows in use: (k, v) or (k, v, r_k), views into the buffers."""
+        n = self.length
+        out = (self.k[:, :, :n], self.v[:, :, :n])
+        return out + ((self.r_k[:, :, :n],) if self.r_k is not None else ())
+
+
 class RMSNorm(nn.Module):
     """y = x / sqrt(mean(x^2) + eps) * weight over the last dimension."""
 
@@ -104,9 +161,13 @@ class RotaryPositionalEmbedding(nn.Module):
         self._cos = self._sin = None
 
     def _table(self, n: int, device, dtype):
-        key = (n, device, dtype)
-        if key != self._cache_key:
-            ang = torch.outer(torch.arange(n, device=device, dtype=dtype),
+        """cos / sin rows of positions 0 .. n-1 (at least): the table is
+        built for the largest length asked so far (doubling), so a decode
+        loop slices it instead of rebuilding it every step."""
+        key = (device, dtype)
+        if key != self._cache_key or self._cos.shape[0] < n:
+            size = n if key != self._cache_key else max(n, 2 * self._cos.shape[0])
+            ang = torch.outer(torch.arange(size, device=device, dtype=dtype),
                               self.inv_freq.to(device=device, dtype=dtype))
             ang = torch.cat((ang, ang), dim=-1)
             self._cos, self._sin, self._cache_key = ang.cos(), ang.sin(), key
@@ -290,6 +351,8 @@ class NaylisAttention(nn.Module):
         if cu_seqlens_q is not None:
             return self._forward_varlen(x, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
                                         max_seqlen_k)
+        if isinstance(past_kv, StaticKVCache):
+            return self._forward_static(x, mask, past_kv, use_kv_cache)
         B, S, _ = x.shape
         scale = self._attn_scale()
         keep_rk = self.decode_graph_bias
@@ -346,6 +409,56 @@ class NaylisAttention(nn.Module):
                                      bias)
         out = out.transpose(1, 2).contiguous().view(B, S, self.embed_dim)
         return self._finish(out, orig_dtype), new_cache
+
+    def _forward_static(self, x, mask, cache: StaticKVCache, use_kv_cache: bool):
+        """A step against a preallocated cache: an empty cache takes the
+        prompt (the ordinary causal forward, whose k / v / r_k rows are then
+        written into the cache); a nonempty one takes one token, appended in
+        place, and attends to the cache's rows on the decode kernel (or the
+        eager backends, as the tuple cache does)."""
+        B, S, _ = x.shape
+        keep_rk = self.decode_graph_bias
+        if keep_rk and cache.r_k is None:
+            raise ValueError("decode_graph_bias: the StaticKVCache must hold r_k")
+        if cache.length == 0:
+            out, new = self.forward(x, mask, None, True)
+            cache.append(*new)
+            return out, (cache if use_kv_cache else None)
+        if S != 1:
+            raise ValueError("a StaticKVCache with rows in use takes one token per step")
+        scale = self._attn_scale()
+        kernel_decode = (self._use_fna2 and self.soft_cap is None
+                         and not (self.training and self.dropout.p > 0))
+        r_q = r_k = None
+        if kernel_decode:
+            q, k, v, r_q, r_k = self._project(x)
+        else:
+            q = self.q_proj(x).view(B, S, self.num_heads, self.head_dim).transpose(1, 2)
+            k = self.k_proj(x).view(B, S, self.n_kv_heads, self.head_dim).transpose(1, 2)
+            v = self.v_proj(x).view(B, S, self.n_kv_heads, self.head_dim).transpose(1, 2)
+            if keep_rk:
+                r_q, r_k = self._rel(x)
+        if self.use_qk_norm:
+            q, k = self.q_norm(q), self.k_norm(k)
+        if self.rope is not None:
+            q, k = self.rope(q, k, position_offset=cache.length)
+        cache.append(k, v, r_k if keep_rk else None)
+        rows = cache.view()
+        kc, vc = rows[0], rows[1]
+        orig_dtype = q.dtype
+        if q.dtype == torch.float32:
+            q = q.to(torch.bfloat16)
+        if kc.dtype != torch.bfloat16:
+            kc, vc = kc.to(torch.bfloat16), vc.to(torch.bfloat16)
+        if kernel_decode:
+            out = flash_naylis_decode(
+                q, kc, vc, r_q if keep_rk else None, rows[2] if keep_rk else None,
+                self.graph_scale if keep_rk else None, softmax_scale=scale).unsqueeze(2)
+        else:
+            bias = self._cached_bias(r_q, rows[2], q.dtype) if keep_rk else None
+            out = self._attend_eager(x, q, kc, vc, mask, rows, scale, False, False, bias)
+        out = out.transpose(1, 2).contiguous().view(B, S, self.embed_dim)
+        return self._finish(out, orig_dtype), (cache if use_kv_cache else None)
 
     def _rel(self, x: torch.Tensor):
         """R_q, R_k [B, H_G, S, R] in bf16 (attention_fna2.py:301-318)."""

@@ -91,6 +91,49 @@ def test_decode_graph_bias_cache_and_eager_decode():
         m(x[:, 8:], past_kv=cache[:2])
 
 
+def test_static_kv_cache_mechanics():
+    c = A.StaticKVCache.empty(2, 3, 8, 16, graph_heads=2, rank=8, dtype=torch.float32)
+    assert c.capacity == 8 and c.length == 0 and len(c.view()) == 3
+    k = torch.randn(2, 3, 5, 16)
+    v = torch.randn(2, 3, 5, 16)
+    rk = torch.randn(2, 2, 5, 8)
+    c.append(k, v, rk)
+    kv, vv, rv = c.view()
+    assert c.length == 5 and torch.equal(kv, k) and torch.equal(vv, v) and torch.equal(rv, rk)
+    assert kv.data_ptr() == c.k.data_ptr()  # a view: no copy
+    c.append(k[:, :, :3], v[:, :, :3], rk[:, :, :3])
+    assert torch.equal(c.view()[0][:, :, 5:], k[:, :, :3])
+    with pytest.raises(ValueError):
+        c.append(k[:, :, :1], v[:, :, :1], rk[:, :, :1])  # full
+    with pytest.raises(ValueError):
+        A.StaticKVCache.empty(1, 1, 4, 8, 1, 8).append(k[:1, :1, :1, :8], v[:1, :1, :1, :8])
+
+
+@pytest.mark.parametrize("bias", [False, True])
+def test_static_cache_matches_tuple_cache(bias):
+    """Prompt + three decode steps: a StaticKVCache (written in place, bf16)
+    gives the tuple cache's outputs (eager backends, CPU)."""
+    torch.manual_seed(4)
+    m = A.NaylisAttention(128, 4, n_kv_heads=2, rel_rank=8, use_fna2=False,
+                          decode_graph_bias=bias).eval()
+    with torch.no_grad():
+        m.graph_scale.fill_(1.5)
+    x = torch.randn(2, 11, 128)
+    cache = A.StaticKVCache.empty(2, 2, 16, 32, graph_heads=4 if bias else 0, rank=8)
+    with torch.no_grad():
+        y0, tup = m(x[:, :8], use_kv_cache=True)
+        z0, st = m(x[:, :8], past_kv=cache, use_kv_cache=True)
+        assert st is cache and cache.length == 8
+        torch.testing.assert_close(z0, y0)
+        for t in range(8, 11):
+            y, tup = m(x[:, t:t + 1], past_kv=tup, use_kv_cache=True)
+            z, st = m(x[:, t:t + 1], past_kv=cache, use_kv_cache=True)
+            assert (z - y).abs().max().item() < 1e-2
+    assert cache.length == 11
+    with pytest.raises(ValueError):
+        m(x[:, :2], past_kv=cache)  # several tokens against a nonempty cache
+
+
 # ── GPU: the FNA2 path against the module's own eager path ──────────────────
 # The eager reference (bf16 SDPA with a dense bias, and its backward) runs on
 # the CPU; only the FNA2 copy runs on the GPU.
@@ -189,3 +232,25 @@ def test_kernel_decode_step_matches_full_forward_and_reference_decode(gpu):
         assert len(bcache) == 3
         y_bstep, _ = biased(xc[:, 69:], past_kv=bcache)
     assert (y_bstep[:, 0] - y_full[:, 69]).abs().max().item() < 2e-2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bias", [False, True])
+def test_kernel_decode_with_static_cache(gpu, bias):
+    """A StaticKVCache on the GPU: prompt on the FNA2 forward, then decode
+    steps on the decode kernel reading the cache in place; equal to the
+    tuple cache's steps (the same kernel over a torch.cat cache)."""
+    _, fast = _pair(embed_dim=512, num_heads=8, n_kv_heads=2, rel_rank=32, vanilla_heads=2)
+    fast.eval()
+    fast.decode_graph_bias = bias
+    x = torch.randn(2, 40, 512, device="cuda")
+    cache = A.StaticKVCache.empty(2, 2, 64, 64, graph_heads=6 if bias else 0, rank=32,
+                                  device="cuda")
+    with torch.no_grad():
+        _, tup = fast(x[:, :36], use_kv_cache=True)
+        fast(x[:, :36], past_kv=cache, use_kv_cache=True)
+        for t in range(36, 40):
+            y, tup = fast(x[:, t:t + 1], past_kv=tup, use_kv_cache=True)
+            z, _ = fast(x[:, t:t + 1], past_kv=cache, use_kv_cache=True)
+            torch.cuda.synchronize()
+            assert (z - y).abs().max().item() < 2e-2, t
