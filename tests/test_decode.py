@@ -234,3 +234,18 @@ def test_decode_split_count_invariance(gpu):
     for o, l in outs[1:]:
         assert max_abs(o, outs[0][0]) < 1e-2
         assert max_abs(l, outs[0][1]) < 1e-4
+
+
+@pytest.mark.gpu
+def test_decode_long_cache_against_oracle(gpu):
+    """200,000 cached rows (the 64-split cap; Rk of 8 graph heads spans
+    100 MB of one (sequence, KV head)), against the oracle."""
+    from fna2_amd.decode import flash_naylis_decode
+    B, H, HKV, HG, D, R, L = 1, 8, 1, 8, 128, 32, 200_000
+    q, k, v, rq, rk, gs = _case(B, H, HKV, HG, D, R, L, seed=10, device=gpu)
+    seq = torch.tensor([L - 7], dtype=torch.int32, device=gpu)
+    out, lse = flash_naylis_decode(q, k, v, rq, rk, gs, softmax_scale=D ** -0.5,
+                                   cache_seqlens=seq, return_lse=True)
+    torch.cuda.synchronize()
+    ref_o, ref_l = O.decode(q, k, v, rq, rk, gs, D ** -0.5, seqlens=[L - 7])
+    check_out(out, lse, ref_o, ref_l)
