@@ -85,6 +85,8 @@ class FwdArgs(ctypes.Structure):
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
         ("events", ctypes.c_void_p),
+        ("plan", ctypes.c_void_p),
+        ("plan_bytes", ctypes.c_size_t),
     ]
 
 
@@ -115,6 +117,8 @@ class BwdArgs(ctypes.Structure):
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
         ("events", ctypes.c_void_p),
+        ("plan", ctypes.c_void_p),
+        ("plan_bytes", ctypes.c_size_t),
     ]
 
 
@@ -187,6 +191,7 @@ SIGNATURES = {
     "fna2_check_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs)]),
     "fna2_fwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Problem)]),
     "fna2_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Problem)]),
+    "fna2_plan_bytes": (ctypes.c_size_t, [ctypes.POINTER(Problem)]),
     "fna2_fwd": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.c_void_p]),
     "fna2_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), ctypes.c_void_p]),
     "fna2_check_rope": (ctypes.c_int, [ctypes.POINTER(RopeArgs)]),

@@ -41,6 +41,38 @@ struct DqCfg {
   static constexpr int STAGE = KB + RB + VB;
 };
 
+// Gradient rows of tokens outside [cu[0], cu[N]) belong to no tile: with a
+// plan (no list-building launch in the backward) the workgroups of the dQ
+// grid that have no tile zero them, 16 bytes per store.  w of nw: this
+// workgroup among them (the host launches one row of workgroups more than
+// the tile list can fill, so there always are some).
+__device__ void zero_uncovered_rows(const BwdParams& P, int w, int nw) {
+  const Problem& p = P.p;
+  const int cq0 = uni(*const_space(p.cu_q)), cqn = uni(*const_space(p.cu_q + p.nseq));
+  const int ck0 = uni(*const_space(p.cu_k)), ckn = uni(*const_space(p.cu_k + p.nseq));
+  if (cq0 <= 0 && cqn >= p.total_q && ck0 <= 0 && ckn >= p.total_k) return;
+  const int rows = max(p.total_q, p.total_k);
+  const u32x4 z = u32x4{0u, 0u, 0u, 0u};
+  auto clear = [&](const TView& t, int heads, int feat, int64_t row) {
+    for (int h = 0; h < heads; ++h) {
+      uint16_t* r = (uint16_t*)t.ptr + row * t.ss + (int64_t)h * t.sh;
+      for (int f = 0; f < feat; f += 8) st16(r + f, z);
+    }
+  };
+  for (int64_t t = (int64_t)w * blockDim.x + threadIdx.x; t < rows;
+       t += (int64_t)nw * blockDim.x) {
+    if (t < p.total_q && (t < cq0 || t >= cqn)) {
+      clear(P.dq, p.H, p.D, t);
+      if (p.H_G > 0) clear(P.drq, p.H_G, p.R, t);
+    }
+    if (t < p.total_k && (t < ck0 || t >= ckn)) {
+      clear(P.dk, p.H_KV, p.D, t);
+      clear(P.dv, p.H_KV, p.D, t);
+      if (p.H_G > 0) clear(P.drk, p.H_G, p.R, t);
+    }
+  }
+}
+
 template <int D, int RPL>
 __device__ __forceinline__ void dq_body(const BwdParams& P) {
   using C = DqCfg<D, RPL>;
@@ -55,7 +87,11 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   int b, qt;
   SeqExt e;
   if (P.tiles_q) {
-    if (tix >= uni(*const_space(P.n_tiles_q))) return;
+    const int nt = uni(*const_space(P.n_tiles_q));
+    if (tix >= nt) {
+      if (P.zero_uncovered) zero_uncovered_rows(P, (tix - nt) * p.H + h, (int)gridDim.x - nt * p.H);
+      return;
+    }
     tile_decode(P.tiles_q, tix, b, qt, e);
   } else {
     const int nqt = cdiv(p.sq, C::BM);

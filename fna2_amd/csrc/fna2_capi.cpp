@@ -160,6 +160,31 @@ BwdWs bwd_ws(const fna2_problem& p) {
   return w;
 }
 
+// Plan (varlen): the query-tile list the forward and the dQ kernel share
+// (the same tile shape) and the dK/dV key-tile list.
+static_assert(kFwdBM == kDqBM && kFwdBN == kDqBN, "the forward and dQ share their tile list");
+struct PlanLayout {
+  size_t tiles_q = 0, count_q = 0, tiles_k = 0, count_k = 0, bytes = 0;
+};
+PlanLayout plan_layout(const fna2_problem& p) {
+  PlanLayout L;
+  if (!p.varlen || p.batch <= 0) return L;
+  const Grids g = grids(p);
+  size_t off = 0;
+  L.tiles_q = off;
+  off += align_up(sizeof(fna2::TileRec) * (size_t)g.fwd_bound);
+  L.count_q = off;
+  off += kAlign;
+  L.tiles_k = off;
+  off += align_up(sizeof(fna2::TileRec) * (size_t)g.kv_bound);
+  L.count_k = off;
+  off += kAlign;
+  L.bytes = off;
+  return L;
+}
+
+bool use_plan(const void* plan, const fna2_problem& p) { return plan && p.varlen && p.batch > 0; }
+
 fna2::Problem make_problem(const fna2_problem& p) {
   fna2::Problem P;
   std::memset(&P, 0, sizeof(P));
@@ -269,8 +294,11 @@ int fna2_check_fwd(const fna2_fwd_args* a) {
   FNA2_TRY(check_view(a->r_q, p, qw && g, true, 2));
   FNA2_TRY(check_view(a->r_k, p, qw && kw && g, true, 2));
   if (qw && g && !a->graph_scale) return FNA2_E_NULL;
-  if (a->workspace_bytes < fwd_ws(p).bytes || (fwd_ws(p).bytes && !a->workspace))
+  if (use_plan(a->plan, p)) {
+    if (a->plan_bytes < plan_layout(p).bytes || !aligned(a->plan, 32)) return FNA2_E_WORKSPACE;
+  } else if (a->workspace_bytes < fwd_ws(p).bytes || (fwd_ws(p).bytes && !a->workspace)) {
     return FNA2_E_WORKSPACE;
+  }
   return FNA2_OK;
 }
 
@@ -306,6 +334,8 @@ int fna2_check_bwd(const fna2_bwd_args* a) {
     return FNA2_E_SHAPE;
   const BwdWs w = bwd_ws(p);
   if (a->workspace_bytes < w.bytes || !a->workspace) return FNA2_E_WORKSPACE;
+  if (use_plan(a->plan, p) && (a->plan_bytes < plan_layout(p).bytes || !aligned(a->plan, 32)))
+    return FNA2_E_WORKSPACE;
   return FNA2_OK;
 }
 
@@ -317,6 +347,11 @@ size_t fna2_fwd_workspace_bytes(const fna2_problem* p) {
 size_t fna2_bwd_workspace_bytes(const fna2_problem* p) {
   if (!p || check_problem(*p) != FNA2_OK) return 0;
   return bwd_ws(*p).bytes;
+}
+
+size_t fna2_plan_bytes(const fna2_problem* p) {
+  if (!p || check_problem(*p) != FNA2_OK) return 0;
+  return plan_layout(*p).bytes;
 }
 
 int fna2_fwd(const fna2_fwd_args* a, void* stream_ptr) {
@@ -337,7 +372,20 @@ int fna2_fwd(const fna2_fwd_args* a, void* stream_ptr) {
   K.lse = view(a->lse);
   K.gs = a->graph_scale;
   const Grids g = grids(p);
-  if (p.varlen) {
+  if (p.varlen && use_plan(a->plan, p)) {
+    // One launch builds this call's list and the backward's key-tile list.
+    const PlanLayout L = plan_layout(p);
+    char* pl = (char*)a->plan;
+    fna2::TileRec* tiles = (fna2::TileRec*)(pl + L.tiles_q);
+    int* count = (int*)(pl + L.count_q);
+    const fna2::TileList lq{{0, kFwdBM, kFwdBN, 1}, tiles, count, (int)g.fwd_bound};
+    const fna2::TileList lk{{1, kKvBN, kKvBM, 0}, (fna2::TileRec*)(pl + L.tiles_k),
+                            (int*)(pl + L.count_k), (int)g.kv_bound};
+    if (fna2::launch_build_tiles(K.p, lq, &lk, nullptr, stream) != hipSuccess)
+      return FNA2_E_LAUNCH;
+    K.tiles = tiles;
+    K.n_tiles = count;
+  } else if (p.varlen) {
     const FwdWs w = fwd_ws(p);
     fna2::TileRec* tiles = (fna2::TileRec*)((char*)a->workspace + w.tiles);
     int* count = (int*)((char*)a->workspace + w.count);
@@ -397,7 +445,17 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
   K.nlse.sb = p.varlen ? 0 : (int64_t)p.heads * seq_rows;
 
   if (p.batch > 0 && (rows_q(p) > 0 || rows_k(p) > 0)) {
-    if (p.varlen) {
+    if (p.varlen && use_plan(a->plan, p)) {
+      // The forward built both lists; the dQ kernel's spare workgroups zero
+      // the rows no sequence covers.
+      const PlanLayout L = plan_layout(p);
+      const char* pl = (const char*)a->plan;
+      K.tiles_q = (const fna2::TileRec*)(pl + L.tiles_q);
+      K.n_tiles_q = (const int*)(pl + L.count_q);
+      K.tiles_k = (const fna2::TileRec*)(pl + L.tiles_k);
+      K.n_tiles_k = (const int*)(pl + L.count_k);
+      K.zero_uncovered = 1;
+    } else if (p.varlen) {
       fna2::TileRec* tq = (fna2::TileRec*)((char*)a->workspace + w.tiles_q);
       int* cq = (int*)((char*)a->workspace + w.count_q);
       fna2::TileRec* tk = (fna2::TileRec*)((char*)a->workspace + w.tiles_k);
@@ -415,7 +473,10 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
     }
     // dQ first: it also stores delta, which the dK/dV kernel reads.
     if (!mark(a->events, 0, stream)) return FNA2_E_LAUNCH;
-    if (rows_q(p) > 0 && fna2::launch_bwd_dq(K, rpl, (int)g.dq_grid, stream) != hipSuccess)
+    // (with a plan, one more row of workgroups than tiles can fill, so that
+    // spare workgroups exist for the zeroing whatever the lengths)
+    const int dq_grid = (int)g.dq_grid + (K.zero_uncovered ? p.heads : 0);
+    if (rows_q(p) > 0 && fna2::launch_bwd_dq(K, rpl, dq_grid, stream) != hipSuccess)
       return FNA2_E_LAUNCH;
     if (!mark(a->events, 1, stream) || !mark(a->events, 2, stream)) return FNA2_E_LAUNCH;
     // persistent: one workgroup per CU walks the (key tile, KV head) items

@@ -27,6 +27,8 @@ struct BwdParams {
   const int* n_tiles_q;
   const TileRec* tiles_k;  // varlen: key tiles (dK/dV kernel)
   const int* n_tiles_k;
+  int zero_uncovered;  // varlen: the dQ kernel's spare workgroups zero the
+                       // gradient rows of tokens outside every sequence
 };
 
 // Forward tile shape (queries per workgroup / keys per iteration at d = 64;

@@ -192,19 +192,29 @@ def _workspace(fn, prob: _capi.Problem, dev) -> torch.Tensor:
     return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
 
 
-def _run_fwd(prob, q, k, v, r_q, r_k, gs, out, lse, view):
+def new_plan(prob: _capi.Problem, device) -> Optional[torch.Tensor]:
+    """A plan buffer for a varlen problem (None in dense mode): the forward
+    builds the backward's tile lists into it, and the backward given it
+    launches no list builder."""
+    n = int(_capi.lib().fna2_plan_bytes(ctypes.byref(prob)))
+    return torch.empty(n, dtype=torch.uint8, device=device) if n > 0 else None
+
+
+def _run_fwd(prob, q, k, v, r_q, r_k, gs, out, lse, view, plan=None):
     L = _capi.lib()
     ws = _workspace(L.fna2_fwd_workspace_bytes, prob, q.device)
     ev = _events(KernelTimer.FWD)
     args = _capi.FwdArgs(prob, view(q), view(k), view(v), view(r_q), view(r_k), _ptr(gs),
                          view(out), view(lse), ws.data_ptr(), ws.numel(),
                          ctypes.cast(ev, ctypes.c_void_p) if ev is not None else None)
+    if plan is not None:
+        args.plan, args.plan_bytes = plan.data_ptr(), plan.numel()
     with torch.cuda.device(q.device):
         st = L.fna2_fwd(ctypes.byref(args), _stream(q.device))
     _capi.raise_for(st, "fna2_fwd")
 
 
-def _run_bwd(prob, tensors, view):
+def _run_bwd(prob, tensors, view, plan=None):
     (dout, q, k, v, r_q, r_k, gs, out, lse, delta, dq, dk, dv, dr_q, dr_k, d_gs) = tensors
     L = _capi.lib()
     ws = _workspace(L.fna2_bwd_workspace_bytes, prob, q.device)
@@ -213,6 +223,8 @@ def _run_bwd(prob, tensors, view):
                          view(out), view(lse), view(dout), view(delta), view(dq), view(dk),
                          view(dv), view(dr_q), view(dr_k), _ptr(d_gs), ws.data_ptr(), ws.numel(),
                          ctypes.cast(ev, ctypes.c_void_p) if ev is not None else None)
+    if plan is not None:
+        args.plan, args.plan_bytes = plan.data_ptr(), plan.numel()
     with torch.cuda.device(q.device):
         st = L.fna2_bwd(ctypes.byref(args), _stream(q.device))
     _capi.raise_for(st, "fna2_bwd")
@@ -266,8 +278,11 @@ def _fna2_forward_varlen(
     max_seqlen_k: int,
     softmax_scale: float,
     is_causal: bool = True,
+    plan: Optional[torch.Tensor] = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Varlen forward; returns (out [T,H,D], lse [T,H]).  Mirrors :756-804."""
+    """Varlen forward; returns (out [T,H,D], lse [T,H]).  Mirrors :756-804.
+    ``plan`` (from ``new_plan``, optional): also build the backward's tile
+    lists into it, for an ``_fna2_backward_varlen`` given the same plan."""
     total_q, H, D = q.shape
     total_k, H_KV = k.shape[0], k.shape[1]
     H_G = 0 if r_q is None else r_q.shape[1]
@@ -289,7 +304,8 @@ def _fna2_forward_varlen(
     lse = torch.empty(total_q, H, device=q.device, dtype=torch.float32)
     prob = _problem(True, N, max_seqlen_q, max_seqlen_k, total_q, total_k, H, H_KV, H_G, D, R,
                     is_causal, softmax_scale, cu_q, cu_k)
-    _run_fwd(prob, q, k, v, r_q if H_G else None, r_k if H_G else None, gs, out, lse, _view3)
+    _run_fwd(prob, q, k, v, r_q if H_G else None, r_k if H_G else None, gs, out, lse, _view3,
+             plan)
     return out, lse
 
 
@@ -337,8 +353,10 @@ def _fna2_backward_varlen(
     max_seqlen_k: int,
     softmax_scale: float,
     is_causal: bool = True,
+    plan: Optional[torch.Tensor] = None,
 ) -> tuple:
-    """Varlen backward; returns (dq, dk, dv, dr_q, dr_k, d_gs).  Mirrors :1215-1300."""
+    """Varlen backward; returns (dq, dk, dv, dr_q, dr_k, d_gs).  Mirrors :1215-1300.
+    ``plan``: the one the forward of the same problem filled (optional)."""
     total_q, H, D = q.shape
     total_k, H_KV = k.shape[0], k.shape[1]
     H_G = 0 if r_q is None else r_q.shape[1]
@@ -357,8 +375,17 @@ def _fna2_backward_varlen(
     prob = _problem(True, N, max_seqlen_q, max_seqlen_k, total_q, total_k, H, H_KV, H_G, D, R,
                     is_causal, softmax_scale, cu_q, cu_k)
     _run_bwd(prob, (dout, q, k, v, r_q if H_G else None, r_k if H_G else None, gs, out, lse,
-                    delta, dq, dk, dv, dr_q, dr_k, d_gs if H_G else None), _view3)
+                    delta, dq, dk, dv, dr_q, dr_k, d_gs if H_G else None), _view3, plan)
     return dq, dk, dv, dr_q, dr_k, _dgs_out(d_gs, H_G, graph_scale)
+
+
+def _plan_for(q, k, r_q, cu_q, cu_k, max_q, max_k, is_causal, scale):
+    """The plan buffer of a varlen call (its size depends on the shapes only)."""
+    H_G = 0 if r_q is None else r_q.shape[1]
+    R = 0 if r_q is None else r_q.shape[2]
+    prob = _problem(True, cu_q.shape[0] - 1, max_q, max_k, q.shape[0], k.shape[0], q.shape[1],
+                    k.shape[1], H_G, q.shape[2], R, is_causal, scale, cu_q, cu_k)
+    return new_plan(prob, q.device)
 
 
 def _dgs_out(d_gs, H_G, graph_scale):
@@ -389,11 +416,16 @@ class FlashNaylisAttnFunc(torch.autograd.Function):
         if use_varlen:
             if cu_seqlens_k is None:
                 cu_seqlens_k = cu_seqlens_q
+            # The forward's list-building launch also builds the backward's
+            # lists (kept on ctx): the backward then launches no builder.
+            plan = _plan_for(q, k, r_q, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                             max_seqlen_k, is_causal, softmax_scale)
             out, lse = _fna2_forward_varlen(
                 q, k, v, r_q, r_k, graph_scale,
                 cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
-                softmax_scale, is_causal,
+                softmax_scale, is_causal, plan=plan,
             )
+            ctx.plan = plan
         else:
             out, lse = _fna2_forward(q, k, v, r_q, r_k, graph_scale, softmax_scale, is_causal)
         ctx.save_for_backward(q, k, v, r_q, r_k, graph_scale, out, lse)
@@ -413,7 +445,7 @@ class FlashNaylisAttnFunc(torch.autograd.Function):
             grads = _fna2_backward_varlen(
                 dout, q, k, v, r_q, r_k, graph_scale, out, lse,
                 ctx.cu_seqlens_q, ctx.cu_seqlens_k, ctx.max_seqlen_q, ctx.max_seqlen_k,
-                ctx.softmax_scale, ctx.is_causal,
+                ctx.softmax_scale, ctx.is_causal, plan=ctx.plan,
             )
         else:
             grads = _fna2_backward(

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define FNA2_ABI_VERSION 1
+#define FNA2_ABI_VERSION 2
 
 /* Element types.  The attention entry points take FNA2_BF16 (q, k, v, r_q,
  * r_k, out, dout and the gradients); fna2_rope_varlen takes all three. */
@@ -104,6 +104,12 @@ typedef struct fna2_fwd_args {
    * caller; recorded on the stream immediately before and after the
    * attention kernel, for per-kernel timing. */
   void* const* events;
+  /* Optional (varlen; may be NULL): a plan buffer of fna2_plan_bytes.  The
+   * forward's one list-building launch then also builds the backward's
+   * lists into it, and a fna2_bwd given the same plan (and the same
+   * problem) launches no builder: one launch fewer per training step. */
+  void* plan;
+  size_t plan_bytes;
 } fna2_fwd_args;
 
 #define FNA2_FWD_EVENTS 2 /* attention kernel start, end */
@@ -129,6 +135,12 @@ typedef struct fna2_bwd_args {
    * caller, recorded around the dQ/dRq kernel (which also forms delta)
    * and the dK/dV/dRk kernel. */
   void* const* events;
+  /* Optional (varlen; may be NULL): the plan a fna2_fwd of the same problem
+   * filled.  The dQ kernel's spare workgroups then zero the gradient rows
+   * of tokens outside every sequence (the list-building launch does that
+   * without a plan). */
+  const void* plan;
+  size_t plan_bytes;
 } fna2_bwd_args;
 
 /* Varlen rotary position embedding: positions restart at 0 in every packed
@@ -273,6 +285,12 @@ int fna2_check_bwd(const fna2_bwd_args* args);
 /* Workspace bytes the forward / backward need for this problem. */
 size_t fna2_fwd_workspace_bytes(const fna2_problem* p);
 size_t fna2_bwd_workspace_bytes(const fna2_problem* p);
+
+/* Bytes of a plan (the varlen tile lists of the forward and the backward:
+ * device-built, so no host synchronisation); 0 in dense mode.  No
+ * counterpart in the reference, whose varlen grids are (max_seqlen / BLOCK,
+ * H, N) with idle programs (FNA2/flash_naylis_attn.py:784, :1281). */
+size_t fna2_plan_bytes(const fna2_problem* p);
 
 /* Forward: writes out and lse.
  * Replaces _fna2_forward (FNA2/flash_naylis_attn.py:700-753) and

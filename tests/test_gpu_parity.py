@@ -130,10 +130,11 @@ def test_varlen_empty_sequences(gpu):
     _varlen_case(gpu, [0, 40, 0, 0, 90, 0], 2, 64, 2, 2, 16, True, seed=15)
 
 
-def test_varlen_uncovered_rows(gpu):
+@pytest.mark.parametrize("use_plan", [False, True])
+def test_varlen_uncovered_rows(gpu, use_plan):
     """Tokens outside [cu[0], cu[N]) belong to no sequence: zero gradients there
-    (the launch that builds the tile lists also zeroes them), oracle parity
-    inside."""
+    (the launch that builds the tile lists zeroes them; with a plan, the dQ
+    kernel's spare workgroups do), oracle parity inside."""
     F = _fna2()
     lengths = [3, 40, 90, 5]
     (q, k, v, rq, rk, gs_, dout, cu_q, cu_k) = H.make_varlen(lengths, 4, 64, 2, 3, 16, seed=21)
@@ -142,10 +143,16 @@ def test_varlen_uncovered_rows(gpu):
     scale = 0.125
     print(f"varlen uncovered rows: cu {sub.tolist()} of {q.shape[0]} tokens", flush=True)
     g = [t.to(gpu) for t in (q, k, v, rq, rk, gs_, dout, sub)]
+    plan = F._plan_for(g[0], g[1], g[3], g[7], g[7], 90, 90, True, scale) if use_plan else None
+    assert (plan is not None) == use_plan
     out, lse = F._fna2_forward_varlen(g[0], g[1], g[2], g[3], g[4], g[5], g[7], g[7], 90, 90,
-                                      scale, True)
+                                      scale, True, plan=plan)
+    # gradients allocated over garbage, so that only the zeroing makes them 0
+    torch.cuda.empty_cache()
+    junk = torch.full((1 << 20,), float("nan"), device=gpu)
+    del junk
     grads = F._fna2_backward_varlen(g[6], g[0], g[1], g[2], g[3], g[4], g[5], out, lse, g[7],
-                                    g[7], 90, 90, scale, True)
+                                    g[7], 90, 90, scale, True, plan=plan)
     torch.cuda.synchronize()
     ref_out, ref_lse, ref_g = H.oracle_fwd_bwd(q, k, v, rq, rk, gs_, dout, scale, True,
                                                sub.numpy(), sub.numpy())
