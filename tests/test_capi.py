@@ -157,6 +157,22 @@ def test_varlen_workspace_required(lib):
     assert check_fwd(lib, a) == "FNA2_OK"
 
 
+def test_plan_replaces_the_forward_workspace(lib):
+    """A varlen forward given a plan of fna2_plan_bytes needs no workspace of
+    its own; a short or misaligned plan is rejected; dense problems have no
+    plan."""
+    assert lib.fna2_plan_bytes(ctypes.byref(_fwd().p)) == 0
+    a = _fwd(varlen=1, batch=3, total_q=200, total_k=200, cu_seqlens_q=FAKE, cu_seqlens_k=FAKE)
+    need = lib.fna2_plan_bytes(ctypes.byref(a.p))
+    assert need > lib.fna2_fwd_workspace_bytes(ctypes.byref(a.p)) > 0  # plus the key tiles
+    a.plan, a.plan_bytes = FAKE, need - 1
+    assert check_fwd(lib, a) == "FNA2_E_WORKSPACE"
+    a.plan, a.plan_bytes = FAKE + 16, need
+    assert check_fwd(lib, a) == "FNA2_E_WORKSPACE"
+    a.plan, a.plan_bytes = FAKE, need
+    assert check_fwd(lib, a) == "FNA2_OK"
+
+
 def test_fwd_and_bwd_entry_points_reject_before_gpu_work(lib):
     a = _fwd(head_dim=80)
     assert _capi.STATUS[lib.fna2_fwd(ctypes.byref(a), None)] == "FNA2_E_HEAD_DIM"
