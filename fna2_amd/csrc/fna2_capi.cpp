@@ -357,7 +357,8 @@ size_t fna2_plan_bytes(const fna2_problem* p) {
 int fna2_fwd(const fna2_fwd_args* a, void* stream_ptr) {
   FNA2_TRY(fna2_check_fwd(a));
   const fna2_problem& p = a->p;
-  if (rows_q(p) == 0 || p.batch == 0) return FNA2_OK;
+  // A plan is filled even without query rows: the backward relies on it.
+  if (p.batch == 0 || (rows_q(p) == 0 && !use_plan(a->plan, p))) return FNA2_OK;
   FNA2_TRY(check_device());
   hipStream_t stream = (hipStream_t)stream_ptr;
   fna2::FwdParams K;
@@ -383,6 +384,7 @@ int fna2_fwd(const fna2_fwd_args* a, void* stream_ptr) {
                             (int*)(pl + L.count_k), (int)g.kv_bound};
     if (fna2::launch_build_tiles(K.p, lq, &lk, nullptr, stream) != hipSuccess)
       return FNA2_E_LAUNCH;
+    if (rows_q(p) == 0) return FNA2_OK;
     K.tiles = tiles;
     K.n_tiles = count;
   } else if (p.varlen) {
@@ -445,9 +447,10 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
   K.nlse.sb = p.varlen ? 0 : (int64_t)p.heads * seq_rows;
 
   if (p.batch > 0 && (rows_q(p) > 0 || rows_k(p) > 0)) {
-    if (p.varlen && use_plan(a->plan, p)) {
+    if (p.varlen && use_plan(a->plan, p) && rows_q(p) > 0) {
       // The forward built both lists; the dQ kernel's spare workgroups zero
-      // the rows no sequence covers.
+      // the rows no sequence covers.  (Without query rows no dQ kernel runs:
+      // the lists are then built, and the rows zeroed, below.)
       const PlanLayout L = plan_layout(p);
       const char* pl = (const char*)a->plan;
       K.tiles_q = (const fna2::TileRec*)(pl + L.tiles_q);

@@ -230,3 +230,29 @@ def test_row0_equals_v0(gpu):
     q, k, v, rq, rk, gs, _ = H.make_dense(1, 2, 64, 64, 2, 2, 16, seed=4, device=gpu)
     out, _ = F._fna2_forward(q, k, v, rq, rk, gs, 0.125, True)
     assert H.max_abs(out[:, :, 0], v[:, :, 0]) < 1e-2
+
+
+def test_varlen_no_query_rows_with_plan(gpu):
+    """Keys but no query rows: the forward still fills the plan, and the
+    backward (no dQ launch) builds its lists itself and writes zero dK, dV,
+    dRk."""
+    F = _fna2()
+    H_, D, R = 4, 64, 16
+    g = torch.Generator().manual_seed(31)
+    q = torch.randn(0, H_, D, generator=g).bfloat16().to(gpu).requires_grad_(True)
+    k = torch.randn(10, H_, D, generator=g).bfloat16().to(gpu).requires_grad_(True)
+    v = torch.randn(10, H_, D, generator=g).bfloat16().to(gpu).requires_grad_(True)
+    rq = torch.randn(0, H_, R, generator=g).bfloat16().to(gpu).requires_grad_(True)
+    rk = torch.randn(10, H_, R, generator=g).bfloat16().to(gpu).requires_grad_(True)
+    gs_ = torch.ones(H_, device=gpu, requires_grad=True)
+    cu_q = torch.tensor([0, 0, 0], dtype=torch.int32, device=gpu)
+    cu_k = torch.tensor([0, 5, 10], dtype=torch.int32, device=gpu)
+    print("varlen no query rows, with plan", flush=True)
+    out = F.flash_naylis_attn(q, k, v, rq, rk, gs_, softmax_scale=0.125, is_causal=False,
+                              cu_seqlens_q=cu_q, cu_seqlens_k=cu_k, max_seqlen_q=0,
+                              max_seqlen_k=5)
+    assert out.shape == (0, H_, D)
+    grads = torch.autograd.grad(out, [k, v, rk], torch.zeros_like(out), allow_unused=True)
+    torch.cuda.synchronize()
+    for name, t in zip(("dk", "dv", "drk"), grads):
+        assert t is None or torch.count_nonzero(t.float()) == 0, name
