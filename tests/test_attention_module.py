@@ -254,3 +254,22 @@ def test_kernel_decode_with_static_cache(gpu, bias):
             z, _ = fast(x[:, t:t + 1], past_kv=cache, use_kv_cache=True)
             torch.cuda.synchronize()
             assert (z - y).abs().max().item() < 2e-2, t
+
+
+def test_rope_table_is_sliced_not_rebuilt():
+    """The cos / sin table grows to the longest length asked and is sliced:
+    rotations are the same whichever lengths were asked before (fp32 and
+    bf16, whose table positions are rounded as the reference rounds them)."""
+    for dtype in (torch.float32, torch.bfloat16):
+        torch.manual_seed(5)
+        q = torch.randn(1, 2, 7, 64).to(dtype)
+        k = torch.randn(1, 2, 7, 64).to(dtype)
+        fresh = A.RotaryPositionalEmbedding(64)
+        ref = fresh(q, k, position_offset=300)
+        grown = A.RotaryPositionalEmbedding(64)
+        grown(q[:, :, :1], k[:, :, :1], position_offset=5)     # a short table first
+        grown(q, k, position_offset=1000)                       # then a longer one
+        got = grown(q, k, position_offset=300)
+        assert grown._cos.shape[0] >= 1007
+        torch.testing.assert_close(got[0], ref[0], rtol=0, atol=0)
+        torch.testing.assert_close(got[1], ref[1], rtol=0, atol=0)
