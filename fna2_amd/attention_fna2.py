@@ -43,7 +43,7 @@ import torch.nn.functional as F
 
 from . import _capi
 from .flash_naylis_attn import BLOCK_R, flash_naylis_attn, rank_supported
-from .decode import flash_naylis_decode
+from .decode import decode_supported, flash_naylis_decode
 from .rope import rope_varlen
 
 
@@ -365,7 +365,8 @@ class NaylisAttention(nn.Module):
         # :412-429 decodes with SDPA over torch.cat(past_kv, new)).
         kernel_decode = (self._use_fna2 and past_kv is not None and S == 1
                          and self.soft_cap is None
-                         and not (self.training and self.dropout.p > 0))
+                         and not (self.training and self.dropout.p > 0)
+                         and self._decode_kernel_ok(keep_rk))
         r_q = r_k = None
         if fused or kernel_decode:
             q, k, v, r_q, r_k = self._project(x)
@@ -428,7 +429,8 @@ class NaylisAttention(nn.Module):
             raise ValueError("a StaticKVCache with rows in use takes one token per step")
         scale = self._attn_scale()
         kernel_decode = (self._use_fna2 and self.soft_cap is None
-                         and not (self.training and self.dropout.p > 0))
+                         and not (self.training and self.dropout.p > 0)
+                         and self._decode_kernel_ok(keep_rk))
         r_q = r_k = None
         if kernel_decode:
             q, k, v, r_q, r_k = self._project(x)
@@ -459,6 +461,19 @@ class NaylisAttention(nn.Module):
             out = self._attend_eager(x, q, kc, vc, mask, rows, scale, False, False, bias)
         out = out.transpose(1, 2).contiguous().view(B, S, self.embed_dim)
         return self._finish(out, orig_dtype), (cache if use_kv_cache else None)
+
+    def _decode_kernel_ok(self, with_bias: bool) -> bool:
+        """The decode kernel serves this head geometry (at most 32 query
+        heads per KV head and, with the cached bias, a group's graph heads x
+        R within one rank tile); other models decode on the eager path, as
+        the reference does."""
+        key = bool(with_bias)
+        cache = self.__dict__.setdefault("_decode_ok_cache", {})
+        if key not in cache:
+            cache[key] = decode_supported(self.num_heads, self.n_kv_heads, self.head_dim,
+                                          self.graph_heads if with_bias else 0,
+                                          self.rel_rank if with_bias else 0)
+        return cache[key]
 
     def _rel(self, x: torch.Tensor):
         """R_q, R_k [B, H_G, S, R] in bf16 (attention_fna2.py:301-318)."""

@@ -141,7 +141,8 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
   const int krow = kw * 32 + l32;   // this lane's key within the item
   const int G = gridDim.x, g = blockIdx.x;
   const int n_items =
-      (P.tiles_k ? uni(*const_space(P.n_tiles_k)) : p.nseq * cdiv(p.sk, C::BN)) * p.H_KV;
+      (P.tiles_k ? min(uni(*const_space(P.n_tiles_k)), P.k_tiles) : p.nseq * cdiv(p.sk, C::BN)) *
+      p.H_KV;
 
   auto decode = [&](int r) {
     KvItem x;

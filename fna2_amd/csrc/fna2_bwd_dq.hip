@@ -87,7 +87,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   int b, qt;
   SeqExt e;
   if (P.tiles_q) {
-    const int nt = uni(*const_space(P.n_tiles_q));
+    const int nt = min(uni(*const_space(P.n_tiles_q)), P.q_tiles);
     if (tix >= nt) {
       if (P.zero_uncovered) zero_uncovered_rows(P, (tix - nt) * p.H + h, (int)gridDim.x - nt * p.H);
       return;

@@ -185,6 +185,56 @@ PlanLayout plan_layout(const fna2_problem& p) {
 
 bool use_plan(const void* plan, const fna2_problem& p) { return plan && p.varlen && p.batch > 0; }
 
+// Plans that fna2_fwd filled, by address, with the problem each was built
+// for.  The tile records carry extents clamped to that problem's token
+// counts and lists sized by its sequence count, so a backward may only read
+// a plan built for the same sequences: fna2_bwd uses a plan found here with
+// a matching key, and otherwise builds its own lists (as without a plan).
+// A small ring: an address reused by a later forward is re-registered.
+uint64_t plan_key(const fna2_problem& p) {
+  const uint64_t f[] = {(uint64_t)p.batch,          (uint64_t)p.total_q,
+                        (uint64_t)p.total_k,        (uint64_t)p.causal,
+                        (uint64_t)(uintptr_t)p.cu_seqlens_q,
+                        (uint64_t)(uintptr_t)p.cu_seqlens_k};
+  uint64_t h = 1469598103934665603ull;  // FNV-1a over the words
+  for (uint64_t w : f) {
+    for (int i = 0; i < 8; ++i) {
+      h ^= (w >> (8 * i)) & 0xffu;
+      h *= 1099511628211ull;
+    }
+  }
+  return h;
+}
+struct PlanEntry {
+  const void* plan;
+  uint64_t key;
+};
+constexpr int kPlanSlots = 256;
+std::mutex g_plan_mu;
+PlanEntry g_plans[kPlanSlots];
+int g_plan_next = 0;
+
+void plan_register(const void* plan, const fna2_problem& p) {
+  std::lock_guard<std::mutex> lk(g_plan_mu);
+  const uint64_t key = plan_key(p);
+  for (PlanEntry& e : g_plans) {
+    if (e.plan == plan) {
+      e.key = key;
+      return;
+    }
+  }
+  g_plans[g_plan_next] = PlanEntry{plan, key};
+  g_plan_next = (g_plan_next + 1) % kPlanSlots;
+}
+
+bool plan_filled_for(const void* plan, const fna2_problem& p) {
+  std::lock_guard<std::mutex> lk(g_plan_mu);
+  const uint64_t key = plan_key(p);
+  for (const PlanEntry& e : g_plans)
+    if (e.plan == plan) return e.key == key;
+  return false;
+}
+
 fna2::Problem make_problem(const fna2_problem& p) {
   fna2::Problem P;
   std::memset(&P, 0, sizeof(P));
@@ -325,12 +375,19 @@ int fna2_check_bwd(const fna2_bwd_args* a) {
   FNA2_TRY(check_view(a->dr_k, p, kw && g, true, 2));
   if (g && (!a->graph_scale || !a->d_graph_scale)) return FNA2_E_NULL;
   // The dK/dV kernel addresses one sequence's query rows of a head with
-  // 32-bit byte offsets.
+  // 32-bit byte offsets.  In varlen mode seqlen_q is only a scheduling hint:
+  // total_q bounds every sequence's length.
+  const uint64_t span_rows =
+      (uint64_t)(p.varlen ? std::max(p.total_q, p.seqlen_q) : p.seqlen_q);
   auto span_ok = [&](const fna2_tensor& t, uint64_t esize) {
     const uint64_t ss = (uint64_t)(t.stride_s < 0 ? -t.stride_s : t.stride_s);
-    return (uint64_t)p.seqlen_q * ss * esize < (1ull << 31);
+    return span_rows * ss * esize < (1ull << 31);
   };
   if (qw && !(span_ok(a->q, 2) && span_ok(a->dout, 2) && span_ok(a->delta, 4)))
+    return FNA2_E_SHAPE;
+  // (the workspace copy of bf16(b Rq), one padded-rank row per query row)
+  if (qw && g && span_rows * (uint64_t)fna2::padded_rank32(p.heads_graph, p.rank) * 2u >=
+                     (1ull << 31))
     return FNA2_E_SHAPE;
   const BwdWs w = bwd_ws(p);
   if (a->workspace_bytes < w.bytes || !a->workspace) return FNA2_E_WORKSPACE;
@@ -384,6 +441,7 @@ int fna2_fwd(const fna2_fwd_args* a, void* stream_ptr) {
                             (int*)(pl + L.count_k), (int)g.kv_bound};
     if (fna2::launch_build_tiles(K.p, lq, &lk, nullptr, stream) != hipSuccess)
       return FNA2_E_LAUNCH;
+    plan_register(a->plan, p);
     if (rows_q(p) == 0) return FNA2_OK;
     K.tiles = tiles;
     K.n_tiles = count;
@@ -433,6 +491,7 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
   const Grids g = grids(p);
   K.dgs_partial = (float*)((char*)a->workspace + w.partial);
   K.q_tiles = (int)g.q_tiles;
+  K.k_tiles = (int)g.kv_tiles;
   const int rpl = fna2::padded_rank32(K.p.H_G, K.p.R);
   // Both are head-major (a head's rows are contiguous): the dK/dV kernel
   // reads them per head, 32 rows at a time.
@@ -447,7 +506,7 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
   K.nlse.sb = p.varlen ? 0 : (int64_t)p.heads * seq_rows;
 
   if (p.batch > 0 && (rows_q(p) > 0 || rows_k(p) > 0)) {
-    if (p.varlen && use_plan(a->plan, p) && rows_q(p) > 0) {
+    if (p.varlen && use_plan(a->plan, p) && rows_q(p) > 0 && plan_filled_for(a->plan, p)) {
       // The forward built both lists; the dQ kernel's spare workgroups zero
       // the rows no sequence covers.  (Without query rows no dQ kernel runs:
       // the lists are then built, and the rows zeroed, below.)
@@ -487,6 +546,11 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
     if (rows_k(p) > 0 && fna2::launch_bwd_dkdv(K, rpl, kv_grid, stream) != hipSuccess)
       return FNA2_E_LAUNCH;
     if (!mark(a->events, 3, stream)) return FNA2_E_LAUNCH;
+  } else if (p.varlen && p.batch == 0 && (rows_q(p) > 0 || rows_k(p) > 0)) {
+    // No sequences: every token lies outside them and gets zero gradients.
+    const fna2::ZeroRows zero{K.dq, K.drq, K.dk, K.dv, K.drk,
+                              (int)std::max(p.total_q, p.total_k)};
+    if (fna2::launch_zero_rows(K.p, zero, stream) != hipSuccess) return FNA2_E_LAUNCH;
   }
   // The dK/dV kernel reduces d_gs when it runs.
   const bool dkdv_ran = p.batch > 0 && rows_k(p) > 0 && g.kv_grid > 0;

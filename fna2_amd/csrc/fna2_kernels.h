@@ -23,6 +23,7 @@ struct BwdParams {
   float* dgs;            // [H_G]
   float* dgs_partial;    // [query tiles][4 waves][H_G] partial sums of d_gs
   int q_tiles;           // query tiles of the dQ grid (varlen: capacity)
+  int k_tiles;           // key tiles (varlen: capacity of the key-tile list)
   const TileRec* tiles_q;  // varlen: query tiles (dQ kernel)
   const int* n_tiles_q;
   const TileRec* tiles_k;  // varlen: key tiles (dK/dV kernel)

@@ -40,6 +40,10 @@ struct ZeroRows {
   int rows;
 };
 
+// Zeroes `zero`'s rows outside [cu[0], cu[N]) (all of them when N = 0),
+// without building a list.
+hipError_t launch_zero_rows(const Problem& p, const ZeroRows& zero, hipStream_t stream);
+
 // Builds up to two lists in one launch (one workgroup each); further
 // workgroups zero `zero`'s rows (1024 tokens each).
 hipError_t launch_build_tiles(const Problem& p, const TileList& a, const TileList* b,

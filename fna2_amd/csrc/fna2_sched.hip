@@ -38,10 +38,12 @@ __device__ __forceinline__ int tile_work(const SeqExt& e, const TileSpec& s,
   return max(cdiv(e.lq, s.step) - lo, 0);
 }
 
-// Zero the gradient rows of token t if it lies outside [cu[0], cu[N]).
+// Zero the gradient rows of token t if it lies outside [cu[0], cu[N])
+// (every token, without sequences: cu may then be null).
 __device__ void zero_row(const Problem& p, const ZeroRows& z, int t) {
-  const int cq0 = p.cu_q[0], cqn = p.cu_q[p.nseq];
-  const int ck0 = p.cu_k[0], ckn = p.cu_k[p.nseq];
+  const bool any = p.nseq > 0;
+  const int cq0 = any ? p.cu_q[0] : 0, cqn = any ? p.cu_q[p.nseq] : 0;
+  const int ck0 = any ? p.cu_k[0] : 0, ckn = any ? p.cu_k[p.nseq] : 0;
   if (t < p.total_q && (t < cq0 || t >= cqn)) {
     for (int h = 0; h < p.H; ++h) {
       uint16_t* r = (uint16_t*)z.dq.ptr + (int64_t)t * z.dq.ss + (int64_t)h * z.dq.sh;
@@ -165,6 +167,15 @@ __global__ __launch_bounds__(kThreads) void build_tiles_kernel(Problem p, TileLi
 }
 
 }  // namespace
+
+hipError_t launch_zero_rows(const Problem& p, const ZeroRows& zero, hipStream_t stream) {
+  if (zero.rows <= 0) return hipSuccess;
+  const int zblocks = (zero.rows + kThreads - 1) / kThreads;
+  const TileList none{{0, 1, 1, 0}, nullptr, nullptr, 0};
+  hipLaunchKernelGGL(build_tiles_kernel, dim3(zblocks), dim3(kThreads), 0, stream, p, none,
+                     none, 0, zero);
+  return hipGetLastError();
+}
 
 hipError_t launch_build_tiles(const Problem& p, const TileList& a, const TileList* b,
                               const ZeroRows* zero, hipStream_t stream) {

@@ -114,6 +114,23 @@ def decode_args(q, k_cache, v_cache, r_q=None, rk_cache=None, graph_scale=None,
     return a, keep, out, lse
 
 
+def decode_supported(heads: int, heads_kv: int, head_dim: int, heads_graph: int = 0,
+                     rank: int = 0) -> bool:
+    """Whether the decode kernel takes this head geometry: the structural
+    limits fna2_check_decode enforces (query heads per KV head <= 32, the
+    graph heads of one KV-head group times R within one 256-wide rank tile,
+    D in {64, 128}), asked of the library itself with an empty batch (a
+    host-only call).  Callers send other shapes to an eager path."""
+    a = _capi.DecodeArgs()
+    a.batch, a.heads, a.heads_kv, a.heads_graph = 0, int(heads), int(heads_kv), int(heads_graph)
+    a.head_dim, a.rank, a.max_seqlen_k, a.num_splits = int(head_dim), int(rank), 0, 0
+    a.softmax_scale = 1.0
+    try:
+        return _capi.lib().fna2_check_decode(ctypes.byref(a)) == 0
+    except (OSError, RuntimeError):
+        return False
+
+
 def flash_naylis_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                         r_q: Optional[torch.Tensor] = None,
                         rk_cache: Optional[torch.Tensor] = None,

@@ -14,9 +14,10 @@
  * The library never allocates device memory: the caller owns every output
  * and the workspace (size it with fna2_*_workspace_bytes).  Kernels are
  * launched on the stream given; no call synchronises the host.  All entry
- * points are stateless and reentrant.  A nonzero return means nothing was
- * launched (FNA2_E_LAUNCH: a launch failed after earlier launches of the
- * same call may already have run).
+ * points are reentrant; the only state is a mutex-guarded record of the
+ * last 256 plans forwards filled (see fna2_bwd_args.plan).  A nonzero return
+ * means nothing was launched (FNA2_E_LAUNCH: a launch failed after earlier
+ * launches of the same call may already have run).
  *
  * Layout.  Each tensor X is described by a base pointer and three element
  * strides (stride_b, stride_s, stride_h); the innermost (feature) stride
@@ -138,7 +139,10 @@ typedef struct fna2_bwd_args {
   /* Optional (varlen; may be NULL): the plan a fna2_fwd of the same problem
    * filled.  The dQ kernel's spare workgroups then zero the gradient rows
    * of tokens outside every sequence (the list-building launch does that
-   * without a plan). */
+   * without a plan).  The library remembers which plans its forwards filled
+   * and for which sequences (cu_seqlens pointers, sequence and token counts,
+   * causal flag); a plan it did not fill for this problem is ignored, and
+   * the backward builds its own lists as without one. */
   const void* plan;
   size_t plan_bytes;
 } fna2_bwd_args;

@@ -234,6 +234,57 @@ def test_kernel_decode_step_matches_full_forward_and_reference_decode(gpu):
     assert (y_bstep[:, 0] - y_full[:, 69]).abs().max().item() < 2e-2
 
 
+def test_decode_kernel_gating_follows_the_library_limits():
+    """The module decodes on the kernel only where fna2_check_decode accepts
+    the head geometry: at most 32 query heads per KV head and, with the cached
+    bias, a group's graph heads x R within one rank tile.  Other models (MQA
+    with 64 heads; 8 graph heads per group at rank 64) take the eager path."""
+    from fna2_amd import _capi
+    from fna2_amd.decode import decode_supported
+    if not _capi.available():
+        pytest.skip("libfna2_hip.so not built")
+    assert decode_supported(16, 4, 128)
+    assert decode_supported(32, 1, 128)
+    assert not decode_supported(64, 1, 128)                 # group 64
+    assert not decode_supported(16, 4, 96)                  # head_dim
+    assert decode_supported(16, 4, 128, 16, 32)             # 4 heads x 32 = 128 wide
+    assert not decode_supported(64, 8, 128, 64, 64)         # 8 heads x 64 = 512 wide
+    assert decode_supported(64, 8, 128, 0, 0)               # same model, no cached bias
+    m = A.NaylisAttention(4096, 64, n_kv_heads=8, rel_rank=64, use_fna2=False)
+    assert m._decode_kernel_ok(False) and not m._decode_kernel_ok(True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kw,bias", [
+    (dict(embed_dim=4096, num_heads=64, n_kv_heads=1, rel_rank=16), False),   # MQA, group 64
+    (dict(embed_dim=1024, num_heads=16, n_kv_heads=2, rel_rank=64), True),    # 8 x 64 rank
+])
+def test_decode_outside_kernel_limits_takes_the_eager_path(gpu, kw, bias):
+    """Head geometries the decode kernel does not take decode on the eager
+    path (as the reference's SDPA step) instead of raising: equal to the
+    eager module's step on the CPU (without the bias) or to the FNA2
+    forward's last row (with it)."""
+    ref, fast = _pair(**kw)
+    ref.eval()
+    fast.eval()
+    assert not fast._decode_kernel_ok(bias)
+    x = torch.randn(2, 24, kw["embed_dim"])
+    xc = x.cuda()
+    with torch.no_grad():
+        if not bias:
+            _, cache = fast(xc[:, :23], use_kv_cache=True)
+            y_step, _ = fast(xc[:, 23:], past_kv=cache)
+            _, rcache = ref(x[:, :23], use_kv_cache=True)
+            y_ref, _ = ref(x[:, 23:], past_kv=rcache)
+            assert (y_step.cpu() - y_ref).abs().max().item() < 2e-2
+        else:
+            fast.decode_graph_bias = True
+            y_full, _ = fast(xc)
+            _, bcache = fast(xc[:, :23], use_kv_cache=True)
+            y_bstep, _ = fast(xc[:, 23:], past_kv=bcache)
+            assert (y_bstep[:, 0] - y_full[:, 23]).abs().max().item() < 2e-2
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("bias", [False, True])
 def test_kernel_decode_with_static_cache(gpu, bias):

@@ -202,3 +202,40 @@ def test_python_errors_map_to_assertion(lib):
         _capi.raise_for(-4, "x")
     with pytest.raises(_capi.FNA2Error):
         _capi.raise_for(-10, "x")
+
+
+def _bwd_varlen(total_q, q_row, **over):
+    """A varlen backward call whose q / dout rows are q_row elements apart
+    (e.g. views into one fused projection), 4 heads of 128, rank 32."""
+    p = dict(dtype=1, varlen=1, batch=2, seqlen_q=0, seqlen_k=0, total_q=total_q,
+             total_k=total_q, heads=4, heads_kv=4, heads_graph=4, head_dim=128, rank=32,
+             causal=1, softmax_scale=0.1, cu_seqlens_q=FAKE, cu_seqlens_k=FAKE)
+    p.update(over)
+    b = _capi.BwdArgs()
+    b.p = _capi.Problem(**p)
+    for name in ("q", "k", "v", "out", "dout", "dq", "dk", "dv"):
+        setattr(b, name, _t(ss=q_row, sh=128))
+    for name in ("r_q", "r_k", "dr_q", "dr_k"):
+        setattr(b, name, _t(ss=q_row, sh=32))
+    b.lse = _t(ss=4, sh=1)
+    b.delta = _t(ss=1, sh=total_q)
+    b.graph_scale = FAKE
+    b.d_graph_scale = FAKE
+    need = _capi.lib().fna2_bwd_workspace_bytes(ctypes.byref(b.p))
+    assert need > 0
+    b.workspace, b.workspace_bytes = FAKE, need
+    return b
+
+
+def test_check_bwd_bounds_varlen_span_by_total_q(lib):
+    """In varlen mode max_seqlen_q is only a hint (0 here): a sequence may
+    span every token, so the dK/dV kernel's 32-bit buffer offsets are bounded
+    with total_q.  28 KB rows (a fused q | k | v | R projection) x 80,000
+    tokens pass 2^31 bytes and must be refused; 70,000 tokens fit."""
+    row = 14336  # elements (28 KB)
+    assert 80000 * row * 2 >= 1 << 31 > 70000 * row * 2
+    big = _bwd_varlen(80000, row)
+    assert _capi.STATUS[lib.fna2_check_bwd(ctypes.byref(big))] == "FNA2_E_SHAPE"
+    assert _capi.STATUS[lib.fna2_bwd(ctypes.byref(big), None)] == "FNA2_E_SHAPE"
+    ok = _bwd_varlen(70000, row)
+    assert _capi.STATUS[lib.fna2_check_bwd(ctypes.byref(ok))] == "FNA2_OK"

@@ -255,4 +255,53 @@ def test_varlen_no_query_rows_with_plan(gpu):
     grads = torch.autograd.grad(out, [k, v, rk], torch.zeros_like(out), allow_unused=True)
     torch.cuda.synchronize()
     for name, t in zip(("dk", "dv", "drk"), grads):
-        assert t is None or torch.count_nonzero(t.float()) == 0, name
+        assert t is not None, f"{name}: the backward did not run"
+        assert torch.count_nonzero(t.float()) == 0, name
+
+
+def test_varlen_no_sequences_zeroes_every_gradient_row(gpu):
+    """cu_seqlens = [0] with tokens present: every token lies outside every
+    sequence, so every gradient row is zero (the reference zero-fills its
+    gradients, FNA2/flash_naylis_attn.py:1247-1252), not left as allocated."""
+    F = _fna2()
+    H_, D, R, T = 4, 64, 16, 37
+    g = torch.Generator().manual_seed(32)
+    mk = lambda *s: torch.randn(*s, generator=g).bfloat16().to(gpu)
+    q, k, v, dout = mk(T, H_, D), mk(T, H_, D), mk(T, H_, D), mk(T, H_, D)
+    rq, rk = mk(T, H_, R), mk(T, H_, R)
+    gs_ = torch.ones(H_, device=gpu)
+    cu = torch.zeros(1, dtype=torch.int32, device=gpu)
+    out, lse = F._fna2_forward_varlen(q, k, v, rq, rk, gs_, cu, cu, 0, 0, 0.125, True)
+    torch.cuda.empty_cache()
+    junk = torch.full((1 << 20,), float("nan"), device=gpu)  # gradients land on garbage
+    del junk
+    print("varlen backward, no sequences, 37 tokens", flush=True)
+    grads = F._fna2_backward_varlen(dout, q, k, v, rq, rk, gs_, out, lse, cu, cu, 0, 0, 0.125,
+                                    True)
+    torch.cuda.synchronize()
+    for name, t in zip(("dq", "dk", "dv", "drq", "drk", "dgs"), grads):
+        assert t is not None, name
+        assert torch.count_nonzero(t.float()) == 0, name
+
+
+def test_backward_ignores_a_plan_no_forward_filled(gpu):
+    """A plan buffer that no forward of this problem filled (here: garbage)
+    is ignored: the backward builds its own tile lists and matches the
+    oracle, instead of reading the garbage as tile records."""
+    F = _fna2()
+    lengths = [70, 3, 200, 129]
+    (q, k, v, rq, rk, gs_, dout, cu_q, cu_k) = H.make_varlen(lengths, 4, 128, 2, 4, 32, seed=33)
+    g = [t.to(gpu) for t in (q, k, v, rq, rk, gs_, dout, cu_q, cu_k)]
+    scale = 0.09
+    out, lse = F._fna2_forward_varlen(g[0], g[1], g[2], g[3], g[4], g[5], g[7], g[8], 200, 200,
+                                      scale, True)
+    plan = F._plan_for(g[0], g[1], g[3], g[7], g[8], 200, 200, True, scale)
+    plan.fill_(0xAB)  # never filled by a forward
+    print("varlen backward with an unfilled plan", flush=True)
+    grads = F._fna2_backward_varlen(g[6], g[0], g[1], g[2], g[3], g[4], g[5], out, lse, g[7],
+                                    g[8], 200, 200, scale, True, plan=plan)
+    torch.cuda.synchronize()
+    ref_out, ref_lse, ref_g = H.oracle_fwd_bwd(q, k, v, rq, rk, gs_, dout, scale, True,
+                                               cu_q.numpy(), cu_k.numpy())
+    H.check_out(out, lse, ref_out, ref_lse)
+    H.check_grads(grads, ref_g)
