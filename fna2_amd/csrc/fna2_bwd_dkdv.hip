@@ -12,26 +12,26 @@
 // The workgroup's 8 waves split the work by role, two waves per SIMD:
 //   * producer wave w (0-3) keeps the K | Rk and V rows of keys 32w..32w+31
 //     in registers (B operands, one key per lane) and per block forms
-//       S, dP  (32 x 32)               A operands: Q | bf16(b Rq) and dO rows
+//       S, dP  (32 x 32)               A operands: Q | Rq and dO rows
 //       P = exp(S - LSE),  dS = P (dP - delta)
 //     and stores P and dS, already in MFMA operand layout, to LDS;
 //   * consumer wave 4 + w holds the fp32 accumulators of the same keys and,
 //     one block behind, forms
 //       dV^T  += dO^T P                A operand: dO^T by transpose reads
-//       acc^T += [Q | bf16(b Rq)]^T dS A operand: the same tiles transposed
-//     and at the end of an item writes dK = a c acc_D, dRk = c acc_R (acc_R
-//     is built from the rank operand bf16(b Rq), so c acc_R = graph_scale
-//     dS^T Rq) and dV.
+//       acc^T += [Q | Rq]^T dS         A operand: the same tiles transposed
+//     and at the end of an item writes dK = a c acc_D, dRk = graph_scale[h]
+//     acc_R (= graph_scale dS^T Rq) and dV.
 // A producer's softmax arithmetic thus overlaps its SIMD partner's MFMAs,
 // and neither role needs more than half of the SIMD's registers.  dK and dV
 // accumulate over the whole GQA group in fp32: no atomics.
 //
-// The dQ kernel stores the rank operand bf16(b Rq), rounded exactly as the
-// forward rounds it, together with delta and -LSE log2(e); the sign/zero
-// factor a of the augmented query rides on the stationary K (exact), so the
-// recomputed S equals the forward's bit for bit.
+// The dQ kernel stores a head-major copy of Rq together with delta and
+// -LSE log2(e); the sign/zero factor a of the augmented query rides on the
+// stationary K (exact), and S is formed as the forward forms it (the rank
+// chain scaled by b = graph_scale[h] / c in fp32, then the head-dim chain),
+// so the recomputed S equals the forward's bit for bit.
 //
-// Q, bf16(b Rq), dO, -LSE log2(e) and delta tiles stream in by DMA (issued by
+// Q, Rq, dO, -LSE log2(e) and delta tiles stream in by DMA (issued by
 // the producers) through a four-stage ring that runs two blocks ahead of the
 // producers, across item boundaries; the consumers read a stage one block
 // later.  The last block of an (item, head) loads the rows of the next one
@@ -258,8 +258,10 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     // Stationary rows (B operands): lane holds key krow, features
     // 16s + 8hl .. +7 of k-step s: K | Rk and V of the producer's (item,
     // head), loaded in place (load16_inplace) and waited for by the ring
-    // barrier.  Rank chunks past R are read as they come and zeroed once the
-    // loads have completed.
+    // barrier.  Rank chunks past R (features R .. padded rank) are read at an
+    // out-of-range offset, so the buffer unit returns zeros: they are never
+    // read from memory (past R lie the next head's rank or, for the last row
+    // of the last graph head, the end of R_k's allocation).
     u32x4 kreg[C::KSD + C::KSR], vreg[C::KSD];
 #pragma unroll
     for (int s = 0; s < C::KSD + C::KSR; ++s) kreg[s] = u32x4{0u, 0u, 0u, 0u};
@@ -286,15 +288,9 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
         load16_inplace<32 * decltype(s)::value>(vreg[s], rv, vo);
       });
       static_for<C::KSR>([&](auto s) {
-        load16_inplace<32 * decltype(s)::value>(kreg[C::KSD + s], rr, ro);
+        const bool in = (2 * decltype(s)::value + hl) * 8 < p.R;
+        load16_inplace<32 * decltype(s)::value>(kreg[C::KSD + s], rr, in ? ro : kOOB);
       });
-    };
-    auto mask_rk = [&]() {
-      if (C::KSR > 0 && (p.R & 15) != 0) {
-#pragma unroll
-        for (int s = 0; s < C::KSR; ++s)
-          if ((2 * s + hl) * 8 >= p.R) kreg[C::KSD + s] = u32x4{0u, 0u, 0u, 0u};
-      }
     };
     // The streamed Q tile is raw, so the factor a in {1, -1, 0} of the
     // augmented operand goes on K (exact): Q (a K)^T = (a Q) K^T.
@@ -307,6 +303,14 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) kreg[s][i] = (kreg[s][i] & kand) ^ kxor;
       }
+    };
+
+    // b = graph_scale[h] / c of the producer's current head (0 for a vanilla
+    // head), set when the cursor enters a head.
+    float bhp = 0.f;
+    auto head_scale = [&](const KvCursor& c) {
+      const int h = c.it.kvh * p.group + c.hi;
+      return uni_f(h < p.H_G ? *const_space(params_here()->gs + h) / p.c : 0.f);
     };
 
     // S and dP of this wave's 32 keys against block qi of the cursor.
@@ -336,18 +340,23 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
         lsr[gq] = *(const f32x4_t*)(ls + 8 * gq + 4 * hl);
         lsr[4 + gq] = *(const f32x4_t*)(ls + 64 + 8 * gq + 4 * hl);
       }
+      // S / c = b Rq Rk^T + Q (a K)^T: the rank chain, scaled by b in fp32,
+      // then the head-dim chain on top, interleaved with the dP chain.
       sacc = f32x16{};
       dpacc = f32x16{};
+#pragma unroll
+      for (int s = 0; s < C::KSR; ++s) sacc = mfma32(qa[C::KSD + s], as_bf16x8(kreg[C::KSD + s]), sacc);
+      if constexpr (C::KSR > 0) sacc *= bhp;
 #pragma unroll
       for (int s = 0; s < C::KSD; ++s) {
         sacc = mfma32(qa[s], as_bf16x8(kreg[s]), sacc);
         dpacc = mfma32(oa[s], as_bf16x8(vreg[s]), dpacc);
       }
-#pragma unroll
-      for (int s = 0; s < C::KSR; ++s) sacc = mfma32(qa[C::KSD + s], as_bf16x8(kreg[C::KSD + s]), sacc);
-      // issue order: every read, then every MFMA
+      // issue order: every read, then the rank MFMAs, then (after the
+      // scaling) the head-dim MFMAs of S and dP
       __builtin_amdgcn_sched_group_barrier(0x100, 2 * C::KSD + C::KSR + 8, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2 * C::KSD + C::KSR, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, C::KSR, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * C::KSD, 0);
     };
     // P = exp(S - LSE) and dS = P (dP - delta) to LDS in the B-operand layout
     // of the consumer's MFMAs: for k-half j (query rows 16j..16j+15), lane
@@ -433,7 +442,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       if (pc.done) return;
       if (pc.qi == 0) {  // rows loaded by the previous block (or above)
         sign_k();
-        mask_rk();
+        bhp = head_scale(pc);
       }
       KvCursor nx = pc;
       advance(nx, no_zero);
@@ -481,12 +490,12 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
 #pragma unroll
     for (int i = 0; i < C::NDB + C::NRB; ++i) dkacc[i] = f32x16{};
 
-    // dRk of head h = c acc_R (zero: an item no query block sees).
+    // dRk of head h = graph_scale[h] acc_R (zero: an item no query block sees).
     auto write_drk = [&](const KvItem& x, int h, bool zero) {
       if constexpr (C::NRB > 0) {
         const int key = x.k0t + krow;
         if (h < p.H_G && key < x.e.lk) {
-          const float sr = zero ? 0.f : p.c;
+          const float sr = zero ? 0.f : *const_space(params_here()->gs + h);
           const TView vd = view_of(&params_here()->drk);
           uint16_t* rrow = seq_base<uint16_t>(vd, p, x.b, x.e.k0, h) + (int64_t)key * vd.ss;
 #pragma unroll

@@ -4,10 +4,10 @@
 // (FNA2/flash_naylis_attn.py:561-693, :1085-1208).
 //
 // One workgroup = 4 waves = 128 queries of one (sequence, head); wave w owns
-// queries 32w..32w+31 with Qa = [a Q | bf16(b Rq)] and dO rows in registers.
+// queries 32w..32w+31 with Qa = [a Q | Rq] and dO rows in registers.
 // The prologue also forms delta = sum_d O dO for these queries (fp32) and
-// stores it, -LSE log2(e) and the rounded bias operand bf16(b Rq) for the
-// dK/dV kernel, which runs after this one.
+// stores it, -LSE log2(e) and a head-major copy of Rq for the dK/dV kernel,
+// which runs after this one.
 // Per key step (keys stream in by DMA through a two-stage ring):
 //   S^T, dP^T  (keys x 32 queries)      A operands: K | Rk and V rows (LDS)
 //   dS^T = P^T (dP^T - delta)
@@ -101,7 +101,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   }
   const int kvh = h / p.group;
   const bool graph = (RPL > 0) && (h < p.H_G);
-  const float bh = graph ? P.gs[h] / p.c : 0.f;
+  const float bh = uni_f(graph ? *const_space(P.gs + h) / p.c : 0.f);
   const int nrs = graph ? cdiv(p.R, 16) : 0;
 
   const uint16_t* qb = seq_base<const uint16_t>(P.q, p, b, e.q0, h);
@@ -172,10 +172,11 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
 #pragma unroll
       for (int s = 0; s < C::KSR; ++s) {
         const bool in = (2 * s + hl) * 8 < p.R;
-        u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rr, in ? vr + 32u * s : kOOB, 0, 0);
-        qreg[C::KSD + s] = as_bf16x8(scale_bf16x8(v, bh));
+        qreg[C::KSD + s] =
+            as_bf16x8(__builtin_amdgcn_raw_buffer_load_b128(rr, in ? vr + 32u * s : kOOB, 0, 0));
       }
-      // The dK/dV kernel streams the same rounded operand bf16(b Rq).
+      // The dK/dV kernel streams Rq from a head-major copy (32 rows of one
+      // head per block, padded to the rank tile width with zeros).
       if (graph && qvalid) {
         uint16_t* srow = seq_base<uint16_t>(P.rqs, p, b, e.q0, h) + (int64_t)qrow * P.rqs.ss;
 #pragma unroll
@@ -236,14 +237,17 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
     bf16x8 db[C::NKB][2];
 #pragma unroll
     for (int kb2 = 0; kb2 < C::NKB; ++kb2) {
+      // S^T / c = b Rk Rq^T + K (a Q)^T: the rank chain, scaled by b in
+      // fp32, then the head-dim chain on top.
       f32x16 sacc = f32x16{}, dpacc = f32x16{};
-#pragma unroll
-      for (int s = 0; s < C::KSD; ++s) sacc = mfma32(row_read<C::BN>(kt, rdl, kb2 * 32, s), qreg[s], sacc);
       if constexpr (C::KSR > 0) {
 #pragma unroll
         for (int s = 0; s < C::KSR; ++s)
           if (s < nrs) sacc = mfma32(row_read<C::BN>(rt, rdl, kb2 * 32, s), qreg[C::KSD + s], sacc);
+        sacc *= bh;
       }
+#pragma unroll
+      for (int s = 0; s < C::KSD; ++s) sacc = mfma32(row_read<C::BN>(kt, rdl, kb2 * 32, s), qreg[s], sacc);
 #pragma unroll
       for (int s = 0; s < C::KSD; ++s) dpacc = mfma32(row_read<C::BN>(vt, rdl, kb2 * 32, s), oreg[s], dpacc);
       // dS^T = P^T (dP^T - delta).  Zero-filled key rows (past the

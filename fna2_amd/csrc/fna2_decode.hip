@@ -18,10 +18,12 @@
 // augmented width D + (graph heads x R):
 //   * Ka's rank part is the concatenation [Rk_h0 | Rk_h1 | ...] of the group's
 //     graph heads;
-//   * Qa's rank part is block diagonal: column i holds
-//     bf16(graph_scale[h] / c * rq_h) only in head i's block;
-// so each head gets its own bias from one contraction.  The online softmax
-// runs per column.  O^T += V^T P^T takes V^T from the row-major V tile
+//   * Qa's rank part is block diagonal: column i holds rq_h only in head
+//     i's block;
+// so each head gets its own bias from one contraction.  The rank chain runs
+// first and its accumulator is scaled per column by graph_scale[h] / c in
+// fp32 before the head-dim chain is added (no rounded operand).  The online
+// softmax runs per column.  O^T += V^T P^T takes V^T from the row-major V tile
 // through ds_read_b64_tr_b16, as in the forward kernel.
 //
 // K, Rk and V tiles are DMA'd global -> LDS (buffer_load ... lds) into a
@@ -147,6 +149,7 @@ __device__ __forceinline__ void decode_body(const DecodeParams& P) {
 
   // Query operand (B of S^T): lane holds Qa[col][16 s + 8 hl .. +7].
   bf16x8 qreg[C::KSD + (RC > 0 ? C::KSR : 0)];
+  float bh = 0.f;  // graph_scale / c of this lane's head column (0: no bias)
   {
     const uint16_t* qb = (const uint16_t*)P.q.ptr + (int64_t)b * P.q.sb + (int64_t)h0 * P.q.sh;
     const auto rs = make_rsrc(qb, 0x7ffffff0u);
@@ -167,15 +170,14 @@ __device__ __forceinline__ void decode_body(const DecodeParams& P) {
                                     (int64_t)h0 * P.rq.sh
                               : qb;
       const auto rr = make_rsrc(rqb, g ? 0x7ffffff0u : 0u);
-      const float bh = g ? P.gs[h0 + col] / P.c : 0.f;
+      bh = g ? P.gs[h0 + col] / P.c : 0.f;
       const uint32_t ro = (uint32_t)col * (uint32_t)P.rq.sh * 2u;
 #pragma unroll
       for (int s = 0; s < C::KSR; ++s) {
         const int c = 2 * s + hl;  // concatenated chunk of this lane
         const bool in = g && c < rch && c / crr == col;
-        u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
-            rr, in ? ro + (uint32_t)(c % crr) * 16u : kOOB, 0, 0);
-        qreg[C::KSD + s] = as_bf16x8(scale_bf16x8(v, bh));
+        qreg[C::KSD + s] = as_bf16x8(__builtin_amdgcn_raw_buffer_load_b128(
+            rr, in ? ro + (uint32_t)(c % crr) * 16u : kOOB, 0, 0));
       }
     }
   }
@@ -196,14 +198,18 @@ __device__ __forceinline__ void decode_body(const DecodeParams& P) {
     const uint8_t* kl = cur;
     const uint8_t* rl = kl + C::KBYTES;
     const uint8_t* vl = rl + C::RBYTES;
+    // S^T / c: the rank chain (block-diagonal Rq: each column sees only its
+    // own head's Rk chunks) scaled per column by that head's b in fp32, then
+    // the head-dim chain on top.
     f32x16 acc = f32x16{};
-#pragma unroll
-    for (int s = 0; s < C::KSD; ++s) acc = mfma32(row_read<kDecBN>(kl, rdl, 0, s), qreg[s], acc);
     if constexpr (RC > 0) {
 #pragma unroll
       for (int s = 0; s < C::KSR; ++s)
         if (s < nrs) acc = mfma32(row_read<kDecBN>(rl, rdl, 0, s), qreg[C::KSD + s], acc);
+      acc *= bh;
     }
+#pragma unroll
+    for (int s = 0; s < C::KSD; ++s) acc = mfma32(row_read<kDecBN>(kl, rdl, 0, s), qreg[s], acc);
     const int kbase = k_lo + t * kDecBN;
     if (kbase + kDecBN > k_hi) {
 #pragma unroll

@@ -2,11 +2,15 @@
 //
 // Conventions used by every kernel in this directory:
 //  * bf16 tensors are addressed as uint16_t; strides are in elements.
-//  * The augmented contraction: for query head h the kernels multiply
-//        Qa_i = [ a * Q_i | b_h * Rq_i ]   with   Ka_j = [ K_j | Rk_j ]
-//    so that S_ij = c * <Qa_i, Ka_j>.  The host picks c > 0 and a in {1,-1,0}
-//    with c * a = softmax_scale; b_h = graph_scale[h] / c.  The Q part is
-//    therefore never rounded, only the bias operand b_h * Rq is (once, to bf16).
+//  * The augmented contraction: for query head h the kernels form
+//        S_ij / c = b_h * <Rq_i, Rk_j> + <a * Q_i, K_j>
+//    as one MFMA accumulator: the rank chain first (bf16 products, exact in
+//    fp32, fp32 sums), that accumulator scaled by b_h in fp32, then the
+//    head-dim chain accumulated on top.  The host picks c > 0 and a in
+//    {1,-1,0} with c * a = softmax_scale; b_h = graph_scale[h] / c.  No
+//    operand is rounded beyond the bf16 inputs (a only flips or clears sign
+//    bits), as in the reference, whose bias is an fp32 dot times graph_scale
+//    in fp32 (FNA2/flash_naylis_attn.py:157-165).
 //  * MFMA: v_mfma_f32_32x32x16_bf16.  Operand lane layout (A rows / B columns
 //    on lane % 32, the 8 k-values of a 16-deep step on lane / 32) and the
 //    accumulator layout (column = lane % 32, row = 8*(v/4) + 4*(lane/32) + v%4
@@ -77,6 +81,9 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 // Marks a value that is the same in every lane as wave-uniform (scalar).
 __device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ float uni_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
+}
 
 // Extents of sequence b (b may differ per lane).
 __device__ __forceinline__ SeqExt seq_ext(const Problem& p, int b) {
@@ -179,14 +186,6 @@ __device__ __forceinline__ float bf16_lo(uint32_t w) {
 }
 __device__ __forceinline__ float bf16_hi(uint32_t w) {
   return __builtin_bit_cast(float, w & 0xffff0000u);
-}
-
-// Eight bf16 values times s, rounded back to bf16.
-__device__ __forceinline__ u32x4 scale_bf16x8(u32x4 v, float s) {
-  u32x4 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) r[i] = pack_bf16(bf16_lo(v[i]) * s, bf16_hi(v[i]) * s);
-  return r;
 }
 
 // Position of row k (0..15) inside a permuted 16-row group (see header).

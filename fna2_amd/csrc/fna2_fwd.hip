@@ -4,7 +4,7 @@
 // (FNA2/flash_naylis_attn.py:58-201, :208-349).
 //
 // One workgroup = 4 waves = 128 queries of one (sequence, head); wave w owns
-// queries 32w..32w+31 and keeps its augmented query operand [a Q | b Rq]
+// queries 32w..32w+31 and keeps its augmented query operand [a Q | Rq]
 // in registers.  Per key step (64 keys at d = 64, 32 at d = 128) the wave
 // computes the transposed score tile S^T = Ka Qa^T (keys x 32 queries) with
 // one MFMA chain over the augmented width D + R (the bias is fused into the
@@ -67,7 +67,7 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
   }
   const int kvh = h / p.group;
   const bool graph = (RPL > 0) && (h < p.H_G);
-  const float bh = graph ? P.gs[h] / p.c : 0.f;
+  const float bh = uni_f(graph ? *const_space(P.gs + h) / p.c : 0.f);
   const int nrs = graph ? cdiv(p.R, 16) : 0;  // rank steps actually used
 
   const uint16_t* qb = seq_base<const uint16_t>(P.q, p, b, e.q0, h);
@@ -136,8 +136,8 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
 #pragma unroll
       for (int s = 0; s < C::KSR; ++s) {
         const bool in = (2 * s + hl) * 8 < p.R;
-        u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rr, in ? ro + 32u * s : kOOB, 0, 0);
-        qreg[C::KSD + s] = as_bf16x8(scale_bf16x8(v, bh));
+        qreg[C::KSD + s] =
+            as_bf16x8(__builtin_amdgcn_raw_buffer_load_b128(rr, in ? ro + 32u * s : kOOB, 0, 0));
       }
     }
   }
@@ -161,18 +161,21 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
     const uint8_t* kl = cur;
     const uint8_t* rl = kl + C::KBYTES;
     const uint8_t* vl = rl + C::RBYTES;
-    // S^T = Ka Qa^T for two 32-key blocks.
+    // S^T / c = b Rk Rq^T + K (a Q)^T per 32-key block: the rank chain
+    // first (exact bf16 products, fp32 sums), its accumulator scaled by b in
+    // fp32, then the head-dim chain added on top.
     f32x16 sacc[C::BN / 32];
 #pragma unroll
     for (int kb2 = 0; kb2 < C::BN / 32; ++kb2) {
       f32x16 acc = f32x16{};
-#pragma unroll
-      for (int s = 0; s < C::KSD; ++s) acc = mfma32(row_read<C::BN>(kl, rdl, kb2 * 32, s), qreg[s], acc);
       if constexpr (C::KSR > 0) {
 #pragma unroll
         for (int s = 0; s < C::KSR; ++s)
           if (s < nrs) acc = mfma32(row_read<C::BN>(rl, rdl, kb2 * 32, s), qreg[C::KSD + s], acc);
+        acc *= bh;
       }
+#pragma unroll
+      for (int s = 0; s < C::KSD; ++s) acc = mfma32(row_read<C::BN>(kl, rdl, kb2 * 32, s), qreg[s], acc);
       sacc[kb2] = acc;
     }
     if ((kbase + C::BN > e.lk) || (p.causal && kbase + C::BN - 1 > wq0)) {

@@ -305,3 +305,49 @@ def test_backward_ignores_a_plan_no_forward_filled(gpu):
                                                cu_q.numpy(), cu_k.numpy())
     H.check_out(out, lse, ref_out, ref_lse)
     H.check_grads(grads, ref_g)
+
+
+@pytest.mark.parametrize("mode", ["varlen", "dense"])
+def test_rank_features_past_r_are_never_read(gpu, mode):
+    """R = 16 with R_q / R_k as views into 32-wide rows whose other 16
+    features are NaN: every kernel must read rank features [0, R) only (a
+    read past R would put 0 * NaN into the scores).  Features past R of the
+    last graph head's last row lie past the end of a dense R_k allocation,
+    so the same rule keeps the kernels inside it."""
+    F = _fna2()
+    Hq, D, R = 4, 64, 16
+    if mode == "varlen":
+        lengths = [90, 33, 257]
+        (q, k, v, rq, rk, gs_, dout, cu_q, cu_k) = H.make_varlen(lengths, Hq, D, 4, 4, R,
+                                                                 seed=41)
+        pad = lambda t: torch.cat([t, torch.full_like(t, float("nan"))], -1)[..., :R]
+    else:
+        q, k, v, rq, rk, gs_, dout = H.make_dense(2, Hq, 160, D, 2, 4, R, seed=42, layout="bshd")
+        # [B, S, H, 2R] memory seen as [B, H, S, R]
+        pad = lambda t: torch.cat([t.transpose(1, 2), torch.full_like(t.transpose(1, 2),
+                                                                      float("nan"))],
+                                  -1)[..., :R].transpose(1, 2)
+    rq_p, rk_p = pad(rq), pad(rk)
+    assert rk_p.stride(-2 if mode == "varlen" else 1) == 2 * R and torch.isnan(
+        rk_p.as_strided((rk_p.numel() * 2,), (1,))).any()
+    scale = 1.0 / math.sqrt(D)
+    print(f"rank views into NaN-padded rows, {mode}", flush=True)
+    dev = [t.to(gpu) for t in (q, k, v, rq_p, rk_p, gs_, dout)]
+    if mode == "varlen":
+        cq, ck = cu_q.to(gpu), cu_k.to(gpu)
+        out, lse = F._fna2_forward_varlen(*dev[:6], cq, ck, 257, 257, scale, False)
+        grads = F._fna2_backward_varlen(dev[6], *dev[:6], out, lse, cq, ck, 257, 257, scale,
+                                        False)
+        cuq, cuk = cu_q.numpy(), cu_k.numpy()
+        causal = False
+    else:
+        out, lse = F._fna2_forward(*dev[:6], scale, True)
+        grads = F._fna2_backward(dev[6], *dev[:6], out, lse, scale, True)
+        cuq = cuk = None
+        causal = True
+    torch.cuda.synchronize()
+    for name, t in zip(("out", "dq", "dk", "dv", "drq", "drk", "dgs"), (out,) + tuple(grads)):
+        assert torch.isfinite(t.float()).all(), f"{name}: non-finite values"
+    ref_out, ref_lse, ref_g = H.oracle_fwd_bwd(q, k, v, rq, rk, gs_, dout, scale, causal, cuq, cuk)
+    H.check_out(out, lse, ref_out, ref_lse)
+    H.check_grads(grads, ref_g)
