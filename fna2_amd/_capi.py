@@ -35,6 +35,7 @@ STATUS = {
     -11: "FNA2_E_DEVICE",
     -12: "FNA2_E_SCALE",
     -13: "FNA2_E_ALIAS",
+    -14: "FNA2_E_SCRATCH",
 }
 # Contract violations surface as AssertionError, like the reference's asserts
 # (FNA2/flash_naylis_attn.py:718-720, :778, :1419-1427); the rest as RuntimeError.
@@ -193,6 +194,8 @@ SIGNATURES = {
     "fna2_bwd_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Problem)]),
     "fna2_plan_bytes": (ctypes.c_size_t, [ctypes.POINTER(Problem)]),
     "fna2_fwd": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.c_void_p]),
+    "fna2_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(FwdArgs), ctypes.c_void_p]),
+    "fna2_fwd_noalloc_max_bytes": (ctypes.c_size_t, []),
     "fna2_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), ctypes.c_void_p]),
     "fna2_check_rope": (ctypes.c_int, [ctypes.POINTER(RopeArgs)]),
     "fna2_rope_varlen": (ctypes.c_int, [ctypes.POINTER(RopeArgs), ctypes.c_void_p]),

@@ -325,6 +325,9 @@ const char* fna2_status_string(int s) {
     case FNA2_E_DEVICE: return "current device is not gfx950";
     case FNA2_E_SCALE: return "softmax_scale must be finite";
     case FNA2_E_ALIAS: return "an output overlaps its input without being equal to it";
+    case FNA2_E_SCRATCH:
+      return "the problem needs more than the allocation-free entry point's static scratch "
+             "(fna2_fwd_noalloc_max_bytes); use fna2_fwd with a workspace";
   }
   return "unknown status";
 }
@@ -411,13 +414,17 @@ size_t fna2_plan_bytes(const fna2_problem* p) {
   return plan_layout(*p).bytes;
 }
 
-int fna2_fwd(const fna2_fwd_args* a, void* stream_ptr) {
-  FNA2_TRY(fna2_check_fwd(a));
+}  // extern "C"
+
+namespace {
+
+// The forward, with its varlen tile list in `ws` (at least fwd_ws(p).bytes;
+// unused with a plan or in dense mode).  `a` has been checked.
+int fwd_launch(const fna2_fwd_args* a, void* ws, hipStream_t stream) {
   const fna2_problem& p = a->p;
   // A plan is filled even without query rows: the backward relies on it.
   if (p.batch == 0 || (rows_q(p) == 0 && !use_plan(a->plan, p))) return FNA2_OK;
   FNA2_TRY(check_device());
-  hipStream_t stream = (hipStream_t)stream_ptr;
   fna2::FwdParams K;
   std::memset(&K, 0, sizeof(K));
   K.p = make_problem(p);
@@ -447,8 +454,8 @@ int fna2_fwd(const fna2_fwd_args* a, void* stream_ptr) {
     K.n_tiles = count;
   } else if (p.varlen) {
     const FwdWs w = fwd_ws(p);
-    fna2::TileRec* tiles = (fna2::TileRec*)((char*)a->workspace + w.tiles);
-    int* count = (int*)((char*)a->workspace + w.count);
+    fna2::TileRec* tiles = (fna2::TileRec*)((char*)ws + w.tiles);
+    int* count = (int*)((char*)ws + w.count);
     const fna2::TileList list{{0, kFwdBM, kFwdBN, 1}, tiles, count, (int)g.fwd_bound};
     if (fna2::launch_build_tiles(K.p, list, nullptr, nullptr, stream) != hipSuccess)
       return FNA2_E_LAUNCH;
@@ -460,6 +467,61 @@ int fna2_fwd(const fna2_fwd_args* a, void* stream_ptr) {
   if (fna2::launch_fwd(K, rpl, (int)g.fwd_grid, stream) != hipSuccess) return FNA2_E_LAUNCH;
   if (!mark(a->events, 1, stream)) return FNA2_E_LAUNCH;
   return FNA2_OK;
+}
+
+// Device memory of the allocation-free forward: the varlen tile list (and
+// its count) that fna2_fwd keeps in the caller's workspace.  Every GPU the
+// library runs on holds its own copy until the process ends.  In host code
+// `scratch` names a host-side stand-in, never its device address: that is
+// resolved per device (hipGetSymbolAddress, with the device current) and
+// only the resolved pointer is handed to kernels.
+constexpr size_t kScratchBytes = (size_t)1 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+int scratch_ptr(void** out) {
+  static std::mutex mu;
+  static void* ptrs[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return FNA2_E_DEVICE;
+  std::lock_guard<std::mutex> lk(mu);
+  if (!ptrs[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr)
+      return FNA2_E_DEVICE;
+    ptrs[dev] = ptr;
+  }
+  *out = ptrs[dev];
+  return FNA2_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fna2_fwd(const fna2_fwd_args* a, void* stream_ptr) {
+  FNA2_TRY(fna2_check_fwd(a));
+  return fwd_launch(a, a->workspace, (hipStream_t)stream_ptr);
+}
+
+size_t fna2_fwd_noalloc_max_bytes(void) { return kScratchBytes; }
+
+int fna2_fwd_noalloc(const fna2_fwd_args* a, void* stream_ptr) {
+  if (!a) return FNA2_E_NULL;
+  // Validate as fna2_fwd would with a workspace of the scratch's size (the
+  // caller's workspace fields are ignored).
+  fna2_fwd_args b = *a;
+  b.workspace = nullptr;
+  b.workspace_bytes = 0;
+  FNA2_TRY(check_problem(b.p));
+  if (!use_plan(b.plan, b.p) && fwd_ws(b.p).bytes > kScratchBytes) return FNA2_E_SCRATCH;
+  void* ws = nullptr;
+  if (!use_plan(b.plan, b.p) && fwd_ws(b.p).bytes > 0) {
+    FNA2_TRY(scratch_ptr(&ws));
+    b.workspace = ws;
+    b.workspace_bytes = kScratchBytes;
+  }
+  FNA2_TRY(fna2_check_fwd(&b));
+  return fwd_launch(&b, ws, (hipStream_t)stream_ptr);
 }
 
 int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {

@@ -12,7 +12,8 @@
  *
  * Every entry point takes plain device pointers, element strides and sizes.
  * The library never allocates device memory: the caller owns every output
- * and the workspace (size it with fna2_*_workspace_bytes).  Kernels are
+ * and the workspace (size it with fna2_*_workspace_bytes); the one exception
+ * is fna2_fwd_noalloc's static 1 MiB array per GPU.  Kernels are
  * launched on the stream given; no call synchronises the host.  All entry
  * points are reentrant; the only state is a mutex-guarded record of the
  * last 256 plans forwards filled (see fna2_bwd_args.plan).  A nonzero return
@@ -58,7 +59,8 @@ enum fna2_status {
   FNA2_E_LAUNCH = -10,     /* a kernel launch failed                         */
   FNA2_E_DEVICE = -11,     /* current device is not gfx950                   */
   FNA2_E_SCALE = -12,      /* softmax_scale not finite                       */
-  FNA2_E_ALIAS = -13       /* an output overlaps its input without equal it  */
+  FNA2_E_ALIAS = -13,      /* an output overlaps its input without equal it  */
+  FNA2_E_SCRATCH = -14     /* beyond fna2_fwd_noalloc's static scratch       */
 };
 
 /* A bf16/fp32 tensor view: base pointer + element strides. */
@@ -300,6 +302,24 @@ size_t fna2_plan_bytes(const fna2_problem* p);
  * Replaces _fna2_forward (FNA2/flash_naylis_attn.py:700-753) and
  * _fna2_forward_varlen (FNA2/flash_naylis_attn.py:756-804). */
 int fna2_fwd(const fna2_fwd_args* args, void* hip_stream);
+
+/* Allocation-free forward.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory, or may not (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  It
+ * is fna2_fwd with the varlen tile list kept in a static device array of
+ * fna2_fwd_noalloc_max_bytes() bytes (1 MiB) that the library holds on every
+ * GPU it runs on, instead of in args->workspace (ignored; a plan, if given,
+ * is used as by fna2_fwd).  Same results as fna2_fwd; the same kernels.
+ * Calls no hipMalloc, hipFree or allocating routine.  A problem whose tile
+ * list needs more (fna2_fwd_workspace_bytes > the maximum, i.e. more than
+ * about 32,000 query tiles: T / 128 + N) returns FNA2_E_SCRATCH.  Every call
+ * on one GPU shares that GPU's array: calls that overlap on one GPU (other
+ * streams, other host threads) race and must be serialised by the caller. */
+int fna2_fwd_noalloc(const fna2_fwd_args* args, void* hip_stream);
+
+/* Bytes of fna2_fwd_noalloc's static scratch (the largest workspace it
+ * stands in for). */
+size_t fna2_fwd_noalloc_max_bytes(void);
 
 /* Backward: writes delta, dq, dk, dv, dr_q, dr_k and d_graph_scale
  * (no pre-zeroing needed; no atomics; bitwise deterministic).
