@@ -486,6 +486,11 @@ def flash_naylis_attn(
     cu_seqlens_*  varlen offsets (int32); max_seqlen_* are scheduling hints
 
     Returns the attention output with q's shape, dtype and strides.
+
+    The call runs the custom operator ``fna2::fwd`` (differentiated by
+    ``fna2::bwd``, ``fna2_amd/ops.py``), which ``torch.compile`` traces;
+    ``FlashNaylisAttnFunc.apply`` with the same arguments computes the same
+    result through a plain ``autograd.Function``, as the reference does.
     """
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
@@ -494,9 +499,10 @@ def flash_naylis_attn(
         assert r_k is not None and r_k.dtype == torch.bfloat16, "r_k must be bfloat16"
         R = r_q.shape[-1]
         assert rank_supported(R), f"rel_rank must be a multiple of 8 in [8, 64] (got {R})"
-    return FlashNaylisAttnFunc.apply(
+    out, _, _ = torch.ops.fna2.fwd(
         q, k, v, r_q, r_k, graph_scale,
-        softmax_scale, is_causal,
+        float(softmax_scale), bool(is_causal),
         cu_seqlens_q, cu_seqlens_k,
-        max_seqlen_q, max_seqlen_k,
+        int(max_seqlen_q), int(max_seqlen_k),
     )
+    return out
