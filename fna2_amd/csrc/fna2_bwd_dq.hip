@@ -302,41 +302,57 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
     if (it + 1 < nkb) step(it + 1, st1, st0);
   }
 
-  // The loop accumulated dS = P (dP - delta); dA = c dS.
+  // The loop accumulated dS = P (dP - delta); dA = c dS.  This lane's part
+  // of the d_gs partial: <Rq_i, (dS Rk)_i> of its query row.
   float gpart = 0.f;
-  if (qvalid) {
-    const float sq = p.qa * p.c;
-    uint16_t* drow = seq_base<uint16_t>(P.dq, p, b, e.q0, h) + (int64_t)qrow * P.dq.ss;
+  if constexpr (C::NRB > 0) {
+    if (graph && qvalid) {
 #pragma unroll
-    for (int d = 0; d < C::NDB; ++d)
+      for (int f = 0; f < C::NRB; ++f)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        u32x2 val;
-        val[0] = pack_bf16(sq * acc[d][4 * g], sq * acc[d][4 * g + 1]);
-        val[1] = pack_bf16(sq * acc[d][4 * g + 2], sq * acc[d][4 * g + 3]);
-        *(u32x2*)(drow + d * 32 + 8 * g + 4 * hl) = val;
-      }
-    if constexpr (C::NRB > 0) {
-      if (graph) {
-        const float sr = bh * p.c;
-        uint16_t* rrow = seq_base<uint16_t>(P.drq, p, b, e.q0, h) + (int64_t)qrow * P.drq.ss;
+        for (int g = 0; g < 4; ++g) {
+          const f32x16& a = acc[C::NDB + f];
+          const u32x2 rv = rq_epi[f][g];
+          if (f * 32 + 8 * g + 4 * hl < p.R)
+            gpart += bf16_lo(rv[0]) * a[4 * g] + bf16_hi(rv[0]) * a[4 * g + 1] +
+                     bf16_lo(rv[1]) * a[4 * g + 2] + bf16_hi(rv[1]) * a[4 * g + 3];
+        }
+    }
+  }
+  // Epilogue: the ring is idle once every wave has left the loop, so each
+  // wave stages its 32 rows of dQ (then of dRq) there (wave w: stage w / 2,
+  // half w % 2) and stores them as whole rows, 16 bytes per lane.
+  using QS = RowStage<D>;
+  static_assert(2 * QS::BYTES <= C::STAGE, "the epilogue staging fits in a ring stage");
+  __syncthreads();
+  uint8_t* obuf = (wv < 2 ? st0 : st1) + (wv & 1) * QS::BYTES;
+  const int nrows = max(min(32, e.lq - wq0), 0);
+  const float sq = p.qa * p.c;
 #pragma unroll
-        for (int f = 0; f < C::NRB; ++f)
+  for (int d = 0; d < C::NDB; ++d)
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int rf = f * 32 + 8 * g + 4 * hl;
-            if (rf < p.R) {
-              const f32x16& a = acc[C::NDB + f];
-              const u32x2 rv = rq_epi[f][g];
-              gpart += bf16_lo(rv[0]) * a[4 * g] + bf16_hi(rv[0]) * a[4 * g + 1] +
-                       bf16_lo(rv[1]) * a[4 * g + 2] + bf16_hi(rv[1]) * a[4 * g + 3];
-              u32x2 val;
-              val[0] = pack_bf16(sr * a[4 * g], sr * a[4 * g + 1]);
-              val[1] = pack_bf16(sr * a[4 * g + 2], sr * a[4 * g + 3]);
-              *(u32x2*)(rrow + rf) = val;
-            }
-          }
-      }
+    for (int g = 0; g < 4; ++g)
+      QS::put4(obuf, l32, d * 32 + 8 * g + 4 * hl, sq * acc[d][4 * g], sq * acc[d][4 * g + 1],
+               sq * acc[d][4 * g + 2], sq * acc[d][4 * g + 3]);
+  QS::store(obuf, seq_base<uint16_t>(P.dq, p, b, e.q0, h) + (int64_t)wq0 * P.dq.ss, P.dq.ss,
+            nrows, QS::CPR, lane);
+  if constexpr (C::NRB > 0) {
+    if (graph) {
+      using RS = RowStage<RPL>;
+      static_assert(RS::BYTES <= QS::BYTES, "dRq rows fit where the dQ rows were");
+      const float sr = bh * p.c;
+#pragma unroll
+      for (int f = 0; f < C::NRB; ++f)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int rf = f * 32 + 8 * g + 4 * hl;
+          const f32x16& a = acc[C::NDB + f];
+          if (rf < p.R)
+            RS::put4(obuf, l32, rf, sr * a[4 * g], sr * a[4 * g + 1], sr * a[4 * g + 2],
+                     sr * a[4 * g + 3]);
+        }
+      RS::store(obuf, seq_base<uint16_t>(P.drq, p, b, e.q0, h) + (int64_t)wq0 * P.drq.ss,
+                P.drq.ss, nrows, p.R / 8, lane);
     }
   }
   // d_gs partial of this wave: sum_i <Rq_i, (dS Rk)_i> over its queries.

@@ -241,8 +241,28 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
   }
 
   const float l_tot = wave_pair_sum(l_i);
-  if (qvalid) {
-    const float inv = 1.f / (l_tot + 1e-6f);
+  const float inv = 1.f / (l_tot + 1e-6f);
+  if constexpr (D == 128) {
+    // Epilogue: the ring is idle once every wave has left the loop, so each
+    // wave stages its 32 rows of O there (wave w: stage w / 2, half w % 2)
+    // and stores them as whole rows, 16 bytes per lane (a lane's own 8-byte
+    // pieces of one row make every store instruction touch 32 partial lines:
+    // c3's forward 90 -> 83 us).
+    using OS = RowStage<D>;
+    static_assert(2 * OS::BYTES <= C::STAGE, "the epilogue staging fits in a ring stage");
+    __syncthreads();
+    uint8_t* obuf = (wv < 2 ? stage0 : stage1) + (wv & 1) * OS::BYTES;
+#pragma unroll
+    for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        OS::put4(obuf, l32, d * 32 + 8 * g + 4 * hl, oacc[d][4 * g] * inv,
+                 oacc[d][4 * g + 1] * inv, oacc[d][4 * g + 2] * inv, oacc[d][4 * g + 3] * inv);
+    OS::store(obuf, seq_base<uint16_t>(P.o, p, b, e.q0, h) + (int64_t)wq0 * P.o.ss, P.o.ss,
+              max(min(32, e.lq - wq0), 0), OS::CPR, lane);
+  } else if (qvalid) {
+    // (At d = 64 staging measured slower on the long dense tiles of c2 and
+    // within noise elsewhere: the rows go out directly.)
     uint16_t* orow = seq_base<uint16_t>(P.o, p, b, e.q0, h) + (int64_t)qrow * P.o.ss;
 #pragma unroll
     for (int d = 0; d < D / 32; ++d)
@@ -253,12 +273,12 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
         val[1] = pack_bf16(oacc[d][4 * g + 2] * inv, oacc[d][4 * g + 3] * inv);
         *(u32x2*)(orow + d * 32 + 8 * g + 4 * hl) = val;
       }
-    if (hl == 0) {
-      float* lrow = seq_base<float>(P.lse, p, b, e.q0, h) + (int64_t)qrow * P.lse.ss;
-      *lrow = (m_i == kNegInf)
-                  ? kNegInf
-                  : m_i * p.c + __builtin_amdgcn_logf(l_tot + 1e-6f) * kLn2;
-    }
+  }
+  if (qvalid && hl == 0) {
+    float* lrow = seq_base<float>(P.lse, p, b, e.q0, h) + (int64_t)qrow * P.lse.ss;
+    *lrow = (m_i == kNegInf)
+                ? kNegInf
+                : m_i * p.c + __builtin_amdgcn_logf(l_tot + 1e-6f) * kLn2;
   }
 }
 

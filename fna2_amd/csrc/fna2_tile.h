@@ -250,6 +250,42 @@ __device__ __forceinline__ bf16x8 tr_operand(const uint8_t* tile, const TrLane& 
   return __builtin_bit_cast(bf16x8, ab);
 }
 
+// Epilogue staging of a wave's 32 output rows of W bf16 values (W a power of
+// two multiple of 8) in LDS, so that global stores write whole rows.  The
+// accumulators hold, per lane, 4 consecutive values of one row (row = lane
+// % 32): row r sits at r * 2W bytes with its 16-byte chunk c at position
+// c ^ (r % (W / 8)), so both the 8-byte writes (32 rows at one chunk) and
+// the 16-byte row reads spread over the banks.
+template <int W>
+struct RowStage {
+  static constexpr int CPR = W / 8;              // 16-byte chunks per row
+  static constexpr int RPI = 64 / CPR;           // rows per wave-wide 16-byte access
+  static constexpr int BYTES = 32 * W * 2;       // one wave's rows
+  static_assert(W >= 8 && (W & (W - 1)) == 0 && RPI >= 1, "row width");
+  __device__ __forceinline__ static int off(int row, int col) {
+    return row * W * 2 + (((col >> 3) ^ (row & (CPR - 1))) << 4) + (col & 7) * 2;
+  }
+  // 4 values (col a multiple of 4) of row `row`.
+  __device__ __forceinline__ static void put4(uint8_t* buf, int row, int col, float a, float b,
+                                              float c, float d) {
+    u32x2 v;
+    v[0] = pack_bf16(a, b);
+    v[1] = pack_bf16(c, d);
+    *(u32x2*)(buf + off(row, col)) = v;
+  }
+  // Stores rows [0, nrows) to dst + row * stride (elements), chunks [0,
+  // valid_chunks) of each: RPI rows per wave-wide access.
+  __device__ __forceinline__ static void store(const uint8_t* buf, uint16_t* dst, int64_t stride,
+                                               int nrows, int valid_chunks, int lane) {
+#pragma unroll
+    for (int i = 0; i < 32 / RPI; ++i) {
+      const int r = i * RPI + lane / CPR, ch = lane % CPR;
+      const u32x4 v = *(const u32x4*)(buf + off(r, ch * 8));
+      if (r < nrows && ch < valid_chunks) st16(dst + (int64_t)r * stride + ch * 8, v);
+    }
+  }
+};
+
 // Ring barrier: wait until at most N of this wave's vector-memory operations
 // (tile DMA included) are in flight and its LDS reads are done, then barrier
 // the workgroup.  Each wave waits for its own DMA before the barrier, so after
