@@ -41,8 +41,12 @@ import statistics
 import sys
 import time
 
-PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (256 CUs x 2.4 GHz x 4096 FLOP/clk)
-PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA, AMD's figure (256 CUs x 2.4 GHz x 4096 FLOP/clk)
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E, AMD's figure
+BF16_FLOP_PER_CLK_CU = 4096  # v_mfma_f32_32x32x16_bf16: 32,768 FLOP per 32 clocks on each of 4 SIMDs
+# hipDeviceAttribute_t values of hip_runtime_api.h (ROCm 7)
+_HIP_ATTR_CLOCK_RATE_KHZ = 5
+_HIP_ATTR_MULTIPROCESSOR_COUNT = 63
 METRIC = "fwd+bwd TFLOP/s & % bf16 MFMA peak, varlen 16k-token pack H=16 d=128 r=32"
 
 
@@ -75,6 +79,52 @@ def parse():
     ap.add_argument("--summarize-counters", nargs=3, metavar=("DB_DIR", "OUT_MD", "COMMAND"),
                     help="write the per-kernel means of a rocprofv3 --pmc pass to OUT_MD")
     return ap.parse_args()
+
+
+def device_peak(dev_index: int = 0) -> dict:
+    """The bf16 dense MFMA peak of the device the bench runs on, derived from
+    its compute-unit count and peak clock (the HIP runtime's attributes),
+    next to AMD's published figure that every fraction in the line uses."""
+    import ctypes
+    import torch
+    cus = torch.cuda.get_device_properties(dev_index).multi_processor_count
+    khz = None
+    for name in ("libamdhip64.so", "libamdhip64.so.7", "libamdhip64.so.6"):
+        try:
+            hip = ctypes.CDLL(name)
+        except OSError:
+            continue
+        v = ctypes.c_int(0)
+        if hip.hipDeviceGetAttribute(ctypes.byref(v), _HIP_ATTR_CLOCK_RATE_KHZ, dev_index) == 0:
+            khz = v.value
+        c = ctypes.c_int(0)
+        if hip.hipDeviceGetAttribute(ctypes.byref(c), _HIP_ATTR_MULTIPROCESSOR_COUNT, dev_index) == 0:
+            cus = c.value or cus
+        break
+    derived = None if not khz else cus * khz * 1e3 * BF16_FLOP_PER_CLK_CU / 1e12
+    return {"published_tflops": PEAK_BF16_TFLOPS, "derived_tflops":
+            None if derived is None else round(derived, 1), "cus": cus,
+            "clock_mhz": None if not khz else khz / 1000.0,
+            "flop_per_clk_cu": BF16_FLOP_PER_CLK_CU}
+
+
+def copy_rate_gbs(nbytes: int = 512 << 20, reps: int = 5) -> float:
+    """Read + write GB/s of a device-to-device copy of nbytes, timed in this
+    run: the practical HBM ceiling next to the 8 TB/s sheet figure."""
+    import torch
+    x = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    y = torch.empty_like(x)
+    y.copy_(x)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        y.copy_(x)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del x, y
+    return 2 * nbytes / (ms * 1e-3) / 1e9
 
 
 COPY_BYTES = 1 << 30
@@ -438,7 +488,11 @@ def rope_bench(args):
 
 def producer_bench(args):
     """q, k, v, R_q, R_k of a c3-sized NaylisAttention (T = 16384, E = 2048,
-    16 heads of 128, 16 graph heads of rank 32, bf16), forward + backward."""
+    16 heads of 128, 16 graph heads of rank 32, bf16), forward + backward:
+    the module's one-GEMM projection over the stacked weights, with separate
+    cotangents (``value``: per-block dW / dx GEMMs, no concatenation) and with
+    cotangents that are column blocks of one buffer (``ms_stacked_grads``: one
+    dx and one dW GEMM), against the reference's five projections."""
     import torch
 
     from fna2_amd import attention_fna2 as A
@@ -463,19 +517,28 @@ def producer_bench(args):
         rk = m.rel_k_proj(x).view(T, HG, R).to(torch.bfloat16).contiguous()
         return q, k, v, rq, rk
 
-    def run(fn):
+    # Cotangents as consecutive column blocks of one [T, E + 2 kv + 2 R]
+    # buffer (what a caller whose gradient producers write one buffer hands
+    # back): the projection's backward is then one dx and one dW GEMM.
+    g_all = torch.randn(T, E + 2 * H * D + 2 * HG * R, device=dev, dtype=torch.bfloat16)
+    stacked = list(torch.split(g_all, [H * D, H * D, H * D, HG * R, HG * R], dim=-1))
+    stacked = [g.view(T, H, D) for g in stacked[:3]] + [g.view(T, HG, R) for g in stacked[3:]]
+
+    def run(fn, cot=grads):
         outs = fn()
-        torch.autograd.grad(outs, [x] + params, grads)
+        torch.autograd.grad(outs, [x] + params, cot)
 
     res = {}
-    for name, fn in (("separate", separate), ("fused", lambda: m._project(x))):
+    for name, fn, cot in (("separate", separate, grads), ("fused", lambda: m._project(x), grads),
+                          ("fused_stacked_grads", lambda: m._project(x), stacked)):
+        run_ = lambda: run(fn, cot)
         for _ in range(args.warmup):
-            run(fn)
+            run_()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(args.steps):
-            run(fn)
+            run_()
         e1.record()
         torch.cuda.synchronize()
         res[name] = e0.elapsed_time(e1) / args.steps
@@ -494,6 +557,7 @@ def producer_bench(args):
                      "traffic": None, "kernel": "hipBLASLt GEMMs"},
         "separate_ms": round(res["separate"], 4),
         "speedup_over_separate": round(res["separate"] / res["fused"], 3),
+        "ms_stacked_grads": round(res["fused_stacked_grads"], 4),
         "cpu_baseline": None,
     }), flush=True)
 
@@ -825,6 +889,10 @@ def main():
         ach = nflops / dur_s / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4)}
+    copy_gbs = copy_rate_gbs()
+    roof["copy_GBps"] = round(copy_gbs, 1)
+    roof["frac_of_copy"] = (round(roof["achieved"] / copy_gbs, 4) if roof["unit"] == "GB/s"
+                            else None)
     roof["traffic"] = measured_traffic(cfg.name, dom)
     roof["traffic_source"] = (f"profiles/traffic_{cfg.name}.json (rocprofv3 FETCH_SIZE + "
                               "WRITE_SIZE per dispatch, copy-calibrated)"
@@ -856,6 +924,7 @@ def main():
                            "(16384 - sum) lies in [64, 512], seed 42" if cfg.name == "c3"
                            else None,
         },
+        "peak_bf16": device_peak(),
         "frac_peak_fwd_bwd": round(tflops / PEAK_BF16_TFLOPS, 4),
         "fwd_tflops": round(fwd_tflops, 2),
         "frac_peak_fwd": round(fwd_tflops / PEAK_BF16_TFLOPS, 4),

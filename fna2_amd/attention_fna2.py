@@ -199,6 +199,104 @@ class RotaryPositionalEmbedding(nn.Module):
         return rope_varlen(q, k, cu_seqlens, self.inv_freq, norm_q, norm_k, eps)
 
 
+def _stacked_view(ws) -> Optional[torch.Tensor]:
+    """The weights as one [sum rows, E] matrix when they are consecutive row
+    blocks of one buffer (no copy), else None."""
+    w0 = ws[0]
+    E = w0.shape[1]
+    if not all(w.dim() == 2 and w.shape[1] == E and w.is_contiguous() and
+               w.dtype == w0.dtype and w.device == w0.device for w in ws):
+        return None
+    st = w0.untyped_storage()
+    off = w0.storage_offset()
+    for w in ws:
+        if w.untyped_storage().data_ptr() != st.data_ptr() or w.storage_offset() != off:
+            return None
+        off += w.numel()
+    rows = sum(w.shape[0] for w in ws)
+    return w0.detach().new_empty(0).set_(st, w0.storage_offset(), (rows, E), (E, 1))
+
+
+def _column_blocks(gs, sizes) -> Optional[torch.Tensor]:
+    """The gradients as one [rows, sum sizes] matrix when they are consecutive
+    column blocks of one buffer with a common row stride (no copy), else None."""
+    if any(g is None for g in gs):
+        return None
+    flat = []
+    for g, n in zip(gs, sizes):
+        try:
+            flat.append(g.view(-1, n))
+        except RuntimeError:
+            return None
+    f0 = flat[0]
+    ld = f0.stride(0)
+    st = f0.untyped_storage().data_ptr()
+    off = f0.storage_offset()
+    for f, n in zip(flat, sizes):
+        if (f.stride(1) != 1 or f.stride(0) != ld or f.shape[0] != f0.shape[0] or
+                f.untyped_storage().data_ptr() != st or f.storage_offset() != off):
+            return None
+        off += n
+    total = sum(sizes)
+    if ld < total:
+        return None
+    return f0.new_empty(0).set_(f0.untyped_storage(), f0.storage_offset(), (f0.shape[0], total),
+                                (ld, 1))
+
+
+class _StackedProjection(torch.autograd.Function):
+    """The projections x W_i^T of weights that are consecutive row blocks of
+    one buffer, as ONE GEMM over the stacked weights; the outputs are column
+    views of its result.  Backward: each dW_i = dY_i^T x is written into its
+    row block of one dW buffer (the parameters' gradients are views of it),
+    and dx is one GEMM when the dY_i are consecutive column blocks of one
+    buffer, else the per-block GEMMs accumulated in place: no concatenation
+    of the weights or of the gradients, and no separate additions."""
+
+    @staticmethod
+    def forward(ctx, x, w_all, sizes, *ws):
+        ctx.save_for_backward(x)
+        ctx.w_all = w_all
+        ctx.sizes = sizes
+        return tuple(torch.split(F.linear(x, w_all), sizes, dim=-1))
+
+    @staticmethod
+    def backward(ctx, *gys):
+        (x,) = ctx.saved_tensors
+        w_all, sizes = ctx.w_all, ctx.sizes
+        E = x.shape[-1]
+        x2 = x.reshape(-1, E)
+        dw_all = torch.empty_like(w_all)
+        dws, r0 = [], 0
+        for g, n in zip(gys, sizes):
+            blk = dw_all[r0:r0 + n]
+            if g is None:
+                blk.zero_()
+            else:
+                torch.mm(g.reshape(-1, n).t(), x2, out=blk)
+            dws.append(blk)
+            r0 += n
+        dx = None
+        if ctx.needs_input_grad[0]:
+            stacked = _column_blocks(gys, sizes)
+            if stacked is not None:
+                dx = torch.mm(stacked, w_all)
+            else:
+                r0 = 0
+                for g, n in zip(gys, sizes):
+                    if g is not None:
+                        g2, w = g.reshape(-1, n), w_all[r0:r0 + n]
+                        if dx is None:
+                            dx = torch.mm(g2, w)
+                        else:
+                            dx.addmm_(g2, w)
+                    r0 += n
+                if dx is None:
+                    dx = torch.zeros_like(x2)
+            dx = dx.view(x.shape)
+        return (dx, None, None, *dws)
+
+
 class NaylisAttention(nn.Module):
     """Token-graph attention: softmax(scale Q K^T + gs_h R_q R_k^T) V per head,
     with R_q, R_k low-rank projections of x for the first H_G = num_heads -
@@ -278,6 +376,11 @@ class NaylisAttention(nn.Module):
         # bias (the reference's cache is (k, v) and its decode step drops the
         # bias).
         self.decode_graph_bias = bool(decode_graph_bias) and graph_heads > 0
+        # The FNA2 path projects x once, over the stacked weights: keep them
+        # as consecutive row blocks of one buffer (the parameters, their
+        # names and the state dict are unchanged).
+        with torch.no_grad():
+            self._pack_projection_weights()
 
     # ── helpers ────────────────────────────────────────────────────────────
     def _attn_scale(self) -> float:
@@ -285,29 +388,58 @@ class NaylisAttention(nn.Module):
             return math.sqrt(self.rope.yarn_scale) / math.sqrt(self.head_dim)
         return 1.0 / math.sqrt(self.head_dim)
 
-    def _project(self, x: torch.Tensor):
-        """q, k, v and (with graph heads) R_q, R_k from ONE GEMM over the
-        stacked weights [W_q; W_k; W_v; W_rq; W_rk]: views into its
-        [.., E + 2 kv_dim + 2 H_G R] output, which the HIP kernels read
-        through their strides.  Replaces the five projections of
-        attention_fna2.py:401-403, :554-556 and _compute_rq_rk(_varlen)
-        (:301-335): x is read once, and R needs no .contiguous() copy.  The
-        parameters stay separate (state dicts unchanged)."""
+    def _projection_weights(self):
         ws = [self.q_proj.weight, self.k_proj.weight, self.v_proj.weight]
         if self.graph_heads > 0:
             ws += [self.rel_q_proj.weight, self.rel_k_proj.weight]
-        y = F.linear(x, torch.cat(ws, dim=0))
+        return ws
+
+    def _pack_projection_weights(self) -> torch.Tensor:
+        """Make the projection weights consecutive row blocks of one buffer
+        (one copy; needed again only after something rebinds a weight, e.g.
+        .to(), a load with assign=True) and return the stacked view."""
+        ws = self._projection_weights()
+        w_all = _stacked_view(ws)
+        if w_all is not None:
+            return w_all
+        w0 = ws[0]
+        buf = torch.empty(sum(w.shape[0] for w in ws), w0.shape[1], dtype=w0.dtype,
+                          device=w0.device)
+        r0 = 0
+        for w in ws:
+            n = w.shape[0]
+            buf[r0:r0 + n].copy_(w.detach())
+            w.data = buf[r0:r0 + n]
+            r0 += n
+        return buf
+
+    def _project(self, x: torch.Tensor):
+        """q, k, v and (with graph heads) R_q, R_k from ONE GEMM over the
+        stacked weights [W_q; W_k; W_v; W_rq; W_rk], which are kept as
+        consecutive row blocks of one buffer (the GEMM reads them in place;
+        the backward is one dx and one dW GEMM).  The outputs are views into
+        the [.., E + 2 kv_dim + 2 H_G R] result, which the HIP kernels read
+        through their strides.  Replaces the five projections of
+        attention_fna2.py:401-403, :554-556 and _compute_rq_rk(_varlen)
+        (:301-335): x is read once, and R needs no .contiguous() copy; in
+        bf16 (the FNA2 path's dtype) R is already bf16, so the reference's
+        .to(torch.bfloat16) is not a pass either.  The parameters stay
+        separate modules (state dicts unchanged)."""
+        with torch.no_grad():
+            w_all = self._pack_projection_weights()
         gr = self.graph_heads * self.rel_rank
         sizes = [self.embed_dim, self.kv_dim, self.kv_dim] + ([gr, gr] if gr else [])
-        parts = list(torch.split(y, sizes, dim=-1))
+        parts = _StackedProjection.apply(x, w_all, sizes, *self._projection_weights())
         lead = x.shape[:-1]
         q = parts[0].view(lead + (self.num_heads, self.head_dim))
         k = parts[1].view(lead + (self.n_kv_heads, self.head_dim))
         v = parts[2].view(lead + (self.n_kv_heads, self.head_dim))
         r_q = r_k = None
         if gr:
-            r_q = parts[3].view(lead + (self.graph_heads, self.rel_rank)).to(torch.bfloat16)
-            r_k = parts[4].view(lead + (self.graph_heads, self.rel_rank)).to(torch.bfloat16)
+            r_q = parts[3].view(lead + (self.graph_heads, self.rel_rank))
+            r_k = parts[4].view(lead + (self.graph_heads, self.rel_rank))
+            if r_q.dtype != torch.bfloat16:  # fp32 activations (the reference casts too)
+                r_q, r_k = r_q.to(torch.bfloat16), r_k.to(torch.bfloat16)
         if x.dim() == 3:  # [B, S, h, *] -> [B, h, S, *]
             q, k, v = (t.transpose(1, 2) for t in (q, k, v))
             if gr:

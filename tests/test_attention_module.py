@@ -324,3 +324,127 @@ def test_rope_table_is_sliced_not_rebuilt():
         assert grown._cos.shape[0] >= 1007
         torch.testing.assert_close(got[0], ref[0], rtol=0, atol=0)
         torch.testing.assert_close(got[1], ref[1], rtol=0, atol=0)
+
+
+def test_stacked_projection_backward_and_weight_buffer():
+    """The projection weights are consecutive row blocks of one buffer (no
+    per-call concatenation); the one-GEMM projection's gradients (x and each
+    weight) equal those of the five separate projections; after .to() the
+    weights are repacked once; the state dict keeps the reference's keys and
+    loads back."""
+    torch.manual_seed(4)
+    m = A.NaylisAttention(64, 4, n_kv_heads=2, rel_rank=8, vanilla_heads=1)
+    ws = m._projection_weights()
+    assert len({w.untyped_storage().data_ptr() for w in ws}) == 1
+    ref = copy.deepcopy(m)
+    x = torch.randn(3, 5, 64)
+    lead = x.shape[:-1]
+    shapes = [(4, 16), (2, 16), (2, 16), (3, 8), (3, 8)]
+    cot = [torch.randn(lead + s_) for s_ in shapes]  # fixed cotangents, [B, S, h, f]
+
+    x1 = x.clone().requires_grad_(True)
+    outs = m._project(x1)
+    loss1 = sum((t.transpose(1, 2).float() * c).sum() for t, c in zip(outs, cot))
+    g1 = torch.autograd.grad(loss1, [x1, *m._projection_weights()])
+
+    x2 = x.clone().requires_grad_(True)
+    mods = [ref.q_proj, ref.k_proj, ref.v_proj, ref.rel_q_proj, ref.rel_k_proj]
+    sep = [mod(x2).view(lead + s_) for mod, s_ in zip(mods, shapes)]
+    sep = sep[:3] + [t.to(torch.bfloat16) for t in sep[3:]]
+    loss2 = sum((t.float() * c).sum() for t, c in zip(sep, cot))
+    g2 = torch.autograd.grad(loss2, [x2, *ref._projection_weights()])
+    for a, b in zip(g1, g2):
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)
+
+    # .to() rebinds each weight; the next projection repacks them once
+    m.to(torch.float64)
+    q64 = m._project(x.double())[0]
+    ws64 = m._projection_weights()
+    assert all(w.dtype == torch.float64 for w in ws64) and q64.dtype == torch.float64
+    assert len({w.untyped_storage().data_ptr() for w in ws64}) == 1
+    sd = m.state_dict()
+    assert {"q_proj.weight", "k_proj.weight", "v_proj.weight", "rel_q_proj.weight",
+            "rel_k_proj.weight"} <= set(sd)
+    m3 = A.NaylisAttention(64, 4, n_kv_heads=2, rel_rank=8, vanilla_heads=1).double()
+    m3.load_state_dict(sd)
+    for a, b in zip(m3._projection_weights(), ws64):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
+def test_module_varlen_bf16_attention_against_oracle(gpu, monkeypatch):
+    """The bf16 module's packed path end to end on the GPU: the one-GEMM
+    projection (R_q / R_k straight from it, no cast), the fused QK-norm +
+    RoPE launch and the attention op.  The attention call's inputs are
+    recorded and its output and the gradients that reach q, k, v, R_q, R_k
+    and graph_scale are checked against the fp64 oracle on those inputs;
+    the projection weights receive gradients."""
+    import numpy as np
+
+    from oracle import fna2_oracle as O
+    from tests import helpers as H
+    torch.manual_seed(8)
+    m = A.NaylisAttention(512, 4, n_kv_heads=2, rel_rank=32, vanilla_heads=1).to(
+        device=gpu, dtype=torch.bfloat16)
+    m._use_fna2 = True
+    with torch.no_grad():
+        m.graph_scale.uniform_(0.5, 1.5)
+    rec = {}
+    real = A._flash_naylis_attn
+
+    def recording(q, k, v, r_q, r_k, gs, **kw):
+        for name, t in (("q", q), ("k", k), ("v", v), ("rq", r_q), ("rk", r_k), ("gs", gs)):
+            t.retain_grad()
+            rec[name] = t
+        out = real(q, k, v, r_q, r_k, gs, **kw)
+        out.register_hook(lambda g: rec.__setitem__("dout", g.detach().clone()))
+        rec["out"], rec["kw"] = out, kw
+        return out
+
+    monkeypatch.setattr(A, "_flash_naylis_attn", recording)
+    lens = [37, 200, 1, 90, 128]
+    T = sum(lens)
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32, device=gpu)
+    x = torch.randn(T, 512, device=gpu, dtype=torch.bfloat16, requires_grad=True)
+    print(f"module varlen bf16 T={T}", flush=True)
+    y, _ = m(x, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=200, max_seqlen_k=200)
+    assert rec["rq"].dtype == torch.bfloat16 and rec["rq"].stride(-1) == 1
+    # R_q / R_k are views into the projection's output, as v is (read in place)
+    assert rec["rq"].untyped_storage().data_ptr() == rec["v"].untyped_storage().data_ptr()
+    y.backward(torch.randn_like(y))
+    torch.cuda.synchronize()
+    cu_np = cu.cpu().numpy()
+    scale = rec["kw"]["softmax_scale"]
+    args = [rec[n].detach() for n in ("q", "k", "v", "rq", "rk", "gs")]
+    ref_out, ref_lse = O.forward(*args, scale, True, cu_np, cu_np)
+    H.check_out(rec["out"], None, ref_out, ref_lse)
+    ref_g = O.backward(rec["dout"], *args, ref_out, ref_lse, scale, True, cu_np, cu_np)
+    got = [rec[n].grad for n in ("q", "k", "v", "rq", "rk", "gs")]
+    H.check_grads(got, ref_g)
+    for w in m._projection_weights():
+        assert w.grad is not None and torch.isfinite(w.grad.float()).all()
+
+
+def test_stacked_projection_gradient_paths_agree():
+    """Backward of the one-GEMM projection: incoming gradients that are
+    consecutive column blocks of one buffer take one dx GEMM; separate ones
+    take per-block GEMMs accumulated in place.  Both give the same dx and
+    dW (each dW a row view of one buffer)."""
+    torch.manual_seed(9)
+    m = A.NaylisAttention(64, 4, n_kv_heads=2, rel_rank=8)
+    ws = m._projection_weights()
+    sizes = [64, 32, 32, 32, 32]
+    x = torch.randn(7, 64, requires_grad=True)
+    w_all = m._pack_projection_weights()
+    outs = A._StackedProjection.apply(x, w_all, sizes, *ws)
+    g_all = torch.randn(7, sum(sizes))
+    blocks = list(torch.split(g_all, sizes, dim=-1))
+    assert A._column_blocks(blocks, sizes) is not None
+    g1 = torch.autograd.grad(outs, [x, *ws], blocks, retain_graph=True)
+    sep = [b.clone() for b in blocks]
+    assert A._column_blocks(sep, sizes) is None
+    g2 = torch.autograd.grad(outs, [x, *ws], sep)
+    for a, b in zip(g1, g2):
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(g1[0], g_all @ w_all, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(torch.cat(g1[1:]), g_all.t() @ x.detach(), rtol=1e-5, atol=1e-5)

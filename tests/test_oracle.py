@@ -250,10 +250,64 @@ def test_eager_reference_bf16_within_reference_tolerance():
     assert np.max(np.abs(out.double().numpy() - ref)) < 0.05
 
 
-def test_flops_formula():
-    fwd, bwd = O.flops([(256, 256)] * 2, H=4, D=64, R=8, causal=True)
-    pairs = 2 * 256 * 257 // 2
-    assert fwd == pairs * 4 * (4 * 64 + 2 * 8) and bwd == pairs * 4 * (10 * 64 + 6 * 8)
+def _visible_pairs_brute(lengths, causal):
+    """Visible (query, key) pairs counted one by one from the oracle's own
+    mask (the one its forward and backward apply)."""
+    total = 0
+    for lq, lk in lengths:
+        if lq and lk:
+            total += int(O._mask(0, lq, lk, causal).sum())
+    return total
+
+
+def _matmul_flops_per_pair(D, R, graph):
+    """FLOPs per visible pair from the products the oracle forms, 2 x inner
+    dimension each: forward S = Q K^T (D), bias Rq Rk^T (R), O = P V (D);
+    backward recomputed S and bias, dP = dO V^T (D), dV = P^T dO (D),
+    dK = dS^T Q (D), dQ = dS K (D), dRq = dS Rk (R), dRk = dS^T Rq (R)."""
+    r = R if graph else 0
+    fwd = 2 * D + 2 * r + 2 * D
+    bwd = (2 * D + 2 * r) + 2 * D + 2 * D + 2 * D + 2 * D + 2 * r + 2 * r
+    return fwd, bwd
+
+
+def test_flops_counts_visible_pairs_by_brute_force():
+    """oracle.flops against a pair-by-pair count of the mask on random
+    length sets (queries and keys of different lengths, empty sequences,
+    causal and not) and the per-pair FLOPs of the oracle's products; with
+    graph and vanilla heads mixed."""
+    rng = np.random.default_rng(17)
+    for causal in (True, False):
+        for _ in range(25):
+            n = int(rng.integers(1, 6))
+            lengths = [(int(rng.integers(0, 70)), int(rng.integers(0, 70))) for _ in range(n)]
+            pairs = _visible_pairs_brute(lengths, causal)
+            H, H_G, D, R = 5, 3, 16, 8
+            fg, bg = _matmul_flops_per_pair(D, R, True)
+            fv, bv = _matmul_flops_per_pair(D, R, False)
+            fwd, bwd = O.flops(lengths, H, D, R, causal, H_G=H_G)
+            assert fwd == pairs * (H_G * fg + (H - H_G) * fv), (lengths, causal)
+            assert bwd == pairs * (H_G * bg + (H - H_G) * bv), (lengths, causal)
+
+
+def test_config_flops_match_brute_force_counts():
+    """The bench's FLOP counts (fna2_amd.configs.Config.flops) equal the
+    brute-force pair count for c2, c3 and c5 (c3 / c5 from their committed
+    packings) and the oracle's count for c4."""
+    from fna2_amd import configs
+    for name in ("c2", "c3", "c5", "c4"):
+        cfg = configs.get(name)
+        lens = [(n, n) for n in cfg.seq_lengths()]
+        if name == "c4":
+            pairs = O.flops(lens, 1, 1, 0, cfg.causal, H_G=0)[0] // 4  # 4D per pair at D = 1
+            assert pairs == 16384 * 16385 // 2
+        elif name == "c5":
+            # the 8192-token sequence is non-causal: all 8192^2 pairs
+            pairs = 8192 * 8192 + _visible_pairs_brute(lens[1:], cfg.causal)
+        else:
+            pairs = _visible_pairs_brute(lens, cfg.causal)
+        f, b = _matmul_flops_per_pair(cfg.D, cfg.R, True)
+        assert cfg.flops() == (pairs * cfg.H * f, pairs * cfg.H * b), name
 
 
 # ── planted mistakes: each must make at least one pinning check fail ──────────
