@@ -66,7 +66,6 @@ struct KvCfg {
   static constexpr int STAGE = QB + RB + OB + LB;
   static constexpr int PW = 4 * 1024;  // a producer's P and dS operands of one block
   static constexpr int PDS = NP * PW;
-  static constexpr int ERS = D * 2 + 16;  // epilogue staging row stride (bytes)
   static constexpr int N_KV = 2 * KSD + KSR;  // stationary-row loads of an item
   using DmaD = Dma<BM, CD, NP>;
   using DmaR = Dma<BM, CR, NP>;
@@ -132,7 +131,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
   __shared__ __attribute__((aligned(1024))) uint8_t st3[C::STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t pd0[C::PDS];
   __shared__ __attribute__((aligned(1024))) uint8_t pd1[C::PDS];
-  __shared__ __attribute__((aligned(16))) uint8_t epi[C::NP * 32 * C::ERS];
+  __shared__ __attribute__((aligned(16))) uint8_t epi[C::NP * RowStage<D>::BYTES];
   const Problem& p = P.p;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = uni(tid >> 6);
@@ -516,28 +515,21 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     };
     // dK = a c acc_D and dV: each wave stages its 32 rows through its own LDS
     // buffer so that a store instruction writes whole rows.
-    uint8_t* obuf = epi + kw * 32 * C::ERS;
+    uint8_t* obuf = epi + kw * RowStage<D>::BYTES;
     auto write_rows = [&](const KvItem& x, const f32x16* acc, float sc, bool zero,
                           const TView& out) {
 #pragma unroll
       for (int d = 0; d < C::NDB; ++d)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          u32x2 val;
-          val[0] = zero ? 0u : pack_bf16(sc * acc[d][4 * q], sc * acc[d][4 * q + 1]);
-          val[1] = zero ? 0u : pack_bf16(sc * acc[d][4 * q + 2], sc * acc[d][4 * q + 3]);
-          *(u32x2*)(obuf + l32 * C::ERS + (d * 32 + 8 * q + 4 * hl) * 2) = val;
+          const f32x16& a = acc[d];
+          RowStage<D>::put4(obuf, l32, d * 32 + 8 * q + 4 * hl, zero ? 0.f : sc * a[4 * q],
+                            zero ? 0.f : sc * a[4 * q + 1], zero ? 0.f : sc * a[4 * q + 2],
+                            zero ? 0.f : sc * a[4 * q + 3]);
         }
-      constexpr int CPR = D / 8;     // 16-byte chunks per row
-      constexpr int RPI = 64 / CPR;  // rows per store instruction
-      uint16_t* base = seq_base<uint16_t>(out, p, x.b, x.e.k0, x.kvh);
-#pragma unroll
-      for (int i = 0; i < 32 / RPI; ++i) {
-        const int r = i * RPI + lane / CPR, ch = lane % CPR;
-        const u32x4 v = *(const u32x4*)(obuf + r * C::ERS + ch * 16);
-        const int key = x.k0t + kw * 32 + r;
-        if (key < x.e.lk) st16(base + (int64_t)key * out.ss + ch * 8, v);
-      }
+      const int k0 = x.k0t + kw * 32;
+      uint16_t* base = seq_base<uint16_t>(out, p, x.b, x.e.k0, x.kvh) + (int64_t)k0 * out.ss;
+      RowStage<D>::store(obuf, base, out.ss, x.e.lk - k0, D / 8, lane);
     };
     auto write_dkdv = [&](const KvItem& x, bool zero) {
       const ParamsPtr pp = params_here();

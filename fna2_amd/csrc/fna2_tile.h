@@ -250,20 +250,39 @@ __device__ __forceinline__ bf16x8 tr_operand(const uint8_t* tile, const TrLane& 
   return __builtin_bit_cast(bf16x8, ab);
 }
 
-// Epilogue staging of a wave's 32 output rows of W bf16 values (W a power of
-// two multiple of 8) in LDS, so that global stores write whole rows.  The
-// accumulators hold, per lane, 4 consecutive values of one row (row = lane
-// % 32): row r sits at r * 2W bytes with its 16-byte chunk c at position
-// c ^ (r % (W / 8)), so both the 8-byte writes (32 rows at one chunk) and
-// the 16-byte row reads spread over the banks.
+// Epilogue staging of a wave's 32 output rows of W bf16 values (W = 32, 64
+// or 128) in LDS, so that global stores write whole rows.  The accumulators
+// hold, per lane, 4 consecutive values of one row (row = lane % 32), so a
+// staging write is an 8-byte write by 32 rows x 2 halves of one 16-byte
+// chunk, and a store reads whole chunks (ds_read_b128) of RPI rows.  Row r
+// sits at r * 2W bytes; its chunk c sits in 16-byte slot pos(r, c) (a
+// permutation of the row's slots), with its two 8-byte halves exchanged
+// when hswap(r) = 1.  The 32 rows of a write then cover 32 distinct (slot,
+// half) pairs, so every 8-byte write and every 16-byte read is free of bank
+// conflicts with 32 banks (16 lanes of a b64 / 8 of a b128 access per
+// cycle) and with 64 banks (32 / 16 lanes per cycle).  (A plain chunk
+// rotation by row, with no half exchange, leaves rows r and r + 16 of a
+// write on the same banks.)  For W = 128 and 64, hswap depends on row bits
+// 3 and 4 only, which a store's lane never sets, so the exchange on reading
+// is a register renaming; for W = 32 it is a per-lane select.
 template <int W>
 struct RowStage {
   static constexpr int CPR = W / 8;              // 16-byte chunks per row
   static constexpr int RPI = 64 / CPR;           // rows per wave-wide 16-byte access
   static constexpr int BYTES = 32 * W * 2;       // one wave's rows
-  static_assert(W >= 8 && (W & (W - 1)) == 0 && RPI >= 1, "row width");
+  static_assert(W == 32 || W == 64 || W == 128, "row width");
+  __device__ __forceinline__ static int pos(int r, int c) {
+    if constexpr (W == 128) return c ^ (r & 15);
+    else if constexpr (W == 64) return c ^ (((r >> 1) & 3) | (((r ^ (r >> 3)) & 1) << 2));
+    else return c ^ ((r >> 2) & 3);
+  }
+  __device__ __forceinline__ static int hswap(int r) {
+    if constexpr (W == 32) return ((r >> 1) ^ (r >> 4)) & 1;
+    else return ((r >> 3) ^ (r >> 4)) & 1;
+  }
+  // Byte offset of values col .. col + 3 (col a multiple of 4) of row `row`.
   __device__ __forceinline__ static int off(int row, int col) {
-    return row * W * 2 + (((col >> 3) ^ (row & (CPR - 1))) << 4) + (col & 7) * 2;
+    return row * W * 2 + (pos(row, col >> 3) << 4) + ((((col >> 2) & 1) ^ hswap(row)) << 3);
   }
   // 4 values (col a multiple of 4) of row `row`.
   __device__ __forceinline__ static void put4(uint8_t* buf, int row, int col, float a, float b,
@@ -280,7 +299,9 @@ struct RowStage {
 #pragma unroll
     for (int i = 0; i < 32 / RPI; ++i) {
       const int r = i * RPI + lane / CPR, ch = lane % CPR;
-      const u32x4 v = *(const u32x4*)(buf + off(r, ch * 8));
+      const u32x4 s = *(const u32x4*)(buf + r * W * 2 + (pos(r, ch) << 4));
+      const bool x = W == 32 ? hswap(r) != 0 : hswap(i * RPI) != 0;
+      const u32x4 v = x ? u32x4{s[2], s[3], s[0], s[1]} : s;
       if (r < nrows && ch < valid_chunks) st16(dst + (int64_t)r * stride + ch * 8, v);
     }
   }
