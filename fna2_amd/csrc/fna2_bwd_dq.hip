@@ -5,9 +5,9 @@
 //
 // One workgroup = 4 waves = 128 queries of one (sequence, head); wave w owns
 // queries 32w..32w+31 with Qa = [a Q | Rq] and dO rows in registers.
-// The prologue also forms delta = sum_d O dO for these queries (fp32) and
-// stores it, -LSE log2(e) and a head-major copy of Rq for the dK/dV kernel,
-// which runs after this one.
+// The prologue also forms delta = sum_d O dO for these queries (fp32); the
+// epilogue stores it, -LSE log2(e) and a head-major copy of Rq for the dK/dV
+// kernel, which runs after this one.
 // Per key step (keys stream in by DMA through a two-stage ring):
 //   S^T, dP^T  (keys x 32 queries)      A operands: K | Rk and V rows (LDS)
 //   dS^T = P^T (dP^T - delta)
@@ -148,7 +148,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   bf16x8 qreg[C::KSD + C::KSR];
   bf16x8 oreg[C::KSD];
   u32x2 rq_epi[C::NRB > 0 ? C::NRB : 1][4];  // raw Rq, accumulator layout (d_gs)
-  float lse2 = 0.f, dl = 0.f;
+  float lse2 = 0.f, dl = 0.f, lse_raw = 0.f;
   {
     const uint32_t rb = (uint32_t)P.q.ss * 2u, orb = (uint32_t)P.dout.ss * 2u;
     const auto rs = make_rsrc(qb + (int64_t)q0 * P.q.ss, (uint32_t)qrows * rb);
@@ -157,6 +157,13 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
     const uint32_t vo = (uint32_t)(wv * 32 + l32) * orb + 16u * hl;
     const uint32_t qxor = p.qa < 0.f ? 0x80008000u : 0u;
     const uint32_t qand = p.qa == 0.f ? 0u : 0xffffffffu;
+    {
+      const uint32_t lrb = (uint32_t)P.lse.ss * 4u;
+      const auto rl = make_rsrc(seq_base<const float>(P.lse, p, b, e.q0, h) + (int64_t)q0 * P.lse.ss,
+                                (uint32_t)qrows * lrb);
+      lse_raw = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(rl, (uint32_t)(wv * 32 + l32) * lrb, 0, 0));
+    }
 #pragma unroll
     for (int s = 0; s < C::KSD; ++s) {
       u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, vq + 32u * s, 0, 0);
@@ -174,13 +181,6 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
         const bool in = (2 * s + hl) * 8 < p.R;
         qreg[C::KSD + s] =
             as_bf16x8(__builtin_amdgcn_raw_buffer_load_b128(rr, in ? vr + 32u * s : kOOB, 0, 0));
-      }
-      // The dK/dV kernel streams Rq from a head-major copy (32 rows of one
-      // head per block, padded to the rank tile width with zeros).
-      if (graph && qvalid) {
-        uint16_t* srow = seq_base<uint16_t>(P.rqs, p, b, e.q0, h) + (int64_t)qrow * P.rqs.ss;
-#pragma unroll
-        for (int s = 0; s < C::KSR; ++s) st16(srow + 16 * s + 8 * hl, as_u32x4(qreg[C::KSD + s]));
       }
 #pragma unroll
       for (int f = 0; f < C::NRB; ++f)
@@ -208,13 +208,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
       }
       dl += __shfl_xor(dl, 32);
     }
-    if (qvalid) {
-      lse2 = seq_base<const float>(P.lse, p, b, e.q0, h)[(int64_t)qrow * P.lse.ss] * kLog2e;
-      if (hl == 0) {
-        seq_base<float>(P.delta, p, b, e.q0, h)[(int64_t)qrow * P.delta.ss] = dl;
-        seq_base<float>(P.nlse, p, b, e.q0, h)[(int64_t)qrow * P.nlse.ss] = -lse2;
-      }
-    }
+    lse2 = lse_raw * kLog2e;
   }
 
   f32x16 acc[C::NDB + C::NRB];
@@ -353,6 +347,23 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
         }
       RS::store(obuf, seq_base<uint16_t>(P.drq, p, b, e.q0, h) + (int64_t)wq0 * P.drq.ss,
                 P.drq.ss, nrows, p.R / 8, lane);
+    }
+  }
+  // For the dK/dV kernel: delta, -LSE log2(e) and the head-major copy of Rq
+  // (32 rows of one head per block, padded to the rank tile width with
+  // zeros).  They are stored here rather than in the prologue, where the
+  // first ring barrier (vmcnt(0)) would wait for the writes to complete.
+  if (qvalid) {
+    if (hl == 0) {
+      seq_base<float>(P.delta, p, b, e.q0, h)[(int64_t)qrow * P.delta.ss] = dl;
+      seq_base<float>(P.nlse, p, b, e.q0, h)[(int64_t)qrow * P.nlse.ss] = -lse2;
+    }
+    if constexpr (C::KSR > 0) {
+      if (graph) {
+        uint16_t* srow = seq_base<uint16_t>(P.rqs, p, b, e.q0, h) + (int64_t)qrow * P.rqs.ss;
+#pragma unroll
+        for (int s = 0; s < C::KSR; ++s) st16(srow + 16 * s + 8 * hl, as_u32x4(qreg[C::KSD + s]));
+      }
     }
   }
   // d_gs partial of this wave: sum_i <Rq_i, (dS Rk)_i> over its queries.
