@@ -140,10 +140,15 @@ def _setup_context(ctx, inputs, output):
     ctx.max_seqlen_q = max_q
     ctx.max_seqlen_k = max_k
     ctx.mark_non_differentiable(lse, plan)
+    # Gradients of lse and plan are never used: without this, autograd would
+    # fill a zero tensor of each (two fill kernels per backward).
+    ctx.set_materialize_grads(False)
 
 
 def _backward(ctx, dout, _dlse, _dplan):
     q, k, v, r_q, r_k, graph_scale, out, lse, plan, cu_q, cu_k = ctx.saved_tensors
+    if dout is None:  # out did not reach the loss
+        return (None,) * 12
     dq, dk, dv, drq, drk, dgs = torch.ops.fna2.bwd(
         dout, q, k, v, r_q, r_k, graph_scale, out, lse, plan, ctx.softmax_scale, ctx.is_causal,
         cu_q, cu_k, ctx.max_seqlen_q, ctx.max_seqlen_k)
