@@ -5,7 +5,8 @@ TrLane.  Checked: the layout is a bijection of 16-byte slots, the DMA plan
 fills every slot with the chunk that belongs there, and both MFMA operand
 reads are free of bank conflicts for 32 and for 64 four-byte banks (one LDS
 cycle serves 128 or 256 bytes: 8 or 16 lanes of a 16-byte read, 16 or 32
-lanes of an 8-byte read).
+lanes of an 8-byte read).  The same checks cover RowStage, the epilogue
+staging layout: its 8-byte accumulator writes and 16-byte row reads.
 """
 from collections import Counter
 
@@ -78,3 +79,64 @@ def test_transpose_reads_conflict_free(nbanks, rows, C):
                     acc.append((a, 8))
                 for ph in range(0, 64, per_cycle):
                     assert max_bank_use(acc[ph:ph + per_cycle], nbanks) == 1
+
+
+# RowStage<W> (epilogue staging of a wave's 32 rows of W bf16 values).
+def stage_pos(W, r, c):
+    if W == 128:
+        return c ^ (r & 15)
+    if W == 64:
+        return c ^ (((r >> 1) & 3) | (((r ^ (r >> 3)) & 1) << 2))
+    return c ^ ((r >> 2) & 3)
+
+
+def stage_hswap(W, r):
+    return ((r >> 1) ^ (r >> 4)) & 1 if W == 32 else ((r >> 3) ^ (r >> 4)) & 1
+
+
+def stage_off(W, row, col):
+    """Byte offset of values col .. col + 3 of `row` (col a multiple of 4)."""
+    return row * W * 2 + (stage_pos(W, row, col >> 3) << 4) + \
+        ((((col >> 2) & 1) ^ stage_hswap(W, row)) << 3)
+
+
+@pytest.mark.parametrize("W", [32, 64, 128])
+def test_row_stage_bijection(W):
+    offs = sorted(stage_off(W, r, col) for r in range(32) for col in range(0, W, 4))
+    assert offs == list(range(0, 32 * W * 2, 8))
+
+
+@pytest.mark.parametrize("nbanks", [32, 64])
+@pytest.mark.parametrize("W", [32, 64, 128])
+def test_row_stage_conflict_free(nbanks, W):
+    # put4: one 8-byte write per lane, lane = (row l32, half hl) at column
+    # 32 d + 8 q + 4 hl; one cycle serves nbanks * 4 / 8 lanes.
+    per_cycle = nbanks * 4 // 8
+    for chunk in range(W // 8):
+        acc = [(stage_off(W, lane & 31, 8 * chunk + 4 * (lane >> 5)), 8) for lane in range(64)]
+        for ph in range(0, 64, per_cycle):
+            assert max_bank_use(acc[ph:ph + per_cycle], nbanks) == 1, (W, chunk, ph)
+    # store: 16-byte reads of whole chunks, RPI rows per instruction, and the
+    # read chunk holds the row's values col .. col + 7 (halves exchanged back)
+    cpr, per_cycle = W // 8, nbanks * 4 // 16
+    rpi = 64 // cpr
+    for i in range(32 // rpi):
+        acc = []
+        for lane in range(64):
+            r, ch = i * rpi + lane // cpr, lane % cpr
+            a = r * W * 2 + (stage_pos(W, r, ch) << 4)
+            lo, hi = stage_off(W, r, 8 * ch), stage_off(W, r, 8 * ch + 4)
+            assert {lo, hi} == {a, a + 8} and (lo == a + 8) == bool(stage_hswap(W, r))
+            if W != 32:  # the exchange is the same for every lane of a store
+                assert stage_hswap(W, r) == stage_hswap(W, i * rpi)
+            acc.append((a, 16))
+        for ph in range(0, 64, per_cycle):
+            assert max_bank_use(acc[ph:ph + per_cycle], nbanks) == 1, (W, i, ph)
+
+
+def test_row_stage_checker_catches_a_plain_rotation():
+    # the chunk rotation alone (no half exchange) leaves rows r, r + 16 on the
+    # same banks of an 8-byte write at 64 banks
+    acc = [((lane & 31) * 256 + ((3 ^ ((lane & 31) & 15)) << 4) + 8 * (lane >> 5), 8)
+           for lane in range(64)]
+    assert max_bank_use(acc[:32], 64) == 2
