@@ -147,7 +147,11 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   // Stationary B operands: Qa and dO rows of this lane's query.
   bf16x8 qreg[C::KSD + C::KSR];
   bf16x8 oreg[C::KSD];
-  u32x2 rq_epi[C::NRB > 0 ? C::NRB : 1][4];  // raw Rq, accumulator layout (d_gs)
+  // d = 64: raw Rq in accumulator layout for the d_gs partial, loaded with
+  // the rows (d = 128 derives it from the query registers at the end, as it
+  // has no registers to spare).
+  constexpr bool RQ_COPY = D == 64 && C::NRB > 0;
+  u32x2 rq_epi[RQ_COPY ? C::NRB : 1][4];
   float lse2 = 0.f, dl = 0.f, lse_raw = 0.f;
   {
     const uint32_t rb = (uint32_t)P.q.ss * 2u, orb = (uint32_t)P.dout.ss * 2u;
@@ -182,14 +186,16 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
         qreg[C::KSD + s] =
             as_bf16x8(__builtin_amdgcn_raw_buffer_load_b128(rr, in ? vr + 32u * s : kOOB, 0, 0));
       }
+      if constexpr (RQ_COPY) {
 #pragma unroll
-      for (int f = 0; f < C::NRB; ++f)
+        for (int f = 0; f < C::NRB; ++f)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int rf = f * 32 + 8 * g + 4 * hl;
-          rq_epi[f][g] = __builtin_amdgcn_raw_buffer_load_b64(
-              rr, rf < p.R ? (uint32_t)(wv * 32 + l32) * rrb + 2u * rf : kOOB, 0, 0);
-        }
+          for (int g = 0; g < 4; ++g) {
+            const int rf = f * 32 + 8 * g + 4 * hl;
+            rq_epi[f][g] = __builtin_amdgcn_raw_buffer_load_b64(
+                rr, rf < p.R ? (uint32_t)(wv * 32 + l32) * rrb + 2u * rf : kOOB, 0, 0);
+          }
+      }
     }
     // delta = sum_d O dO for this lane's query: the lane pair (hl = 0, 1)
     // holds the row's dO chunks, so O is read in the same layout.
@@ -298,19 +304,41 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
 
   // The loop accumulated dS = P (dP - delta); dA = c dS.  This lane's part
   // of the d_gs partial: <Rq_i, (dS Rk)_i> of its query row.
+  // The accumulator holds rank features f*32 + 8g + 4hl + e of this lane's
+  // row (e = 0..3).  At d = 128 they come from the query registers, which
+  // hold features 16s + 8hl .. +7: half of the needed Rq values sit in the
+  // partner lane (lane ^ 32), so each lane passes over the two dwords of
+  // every rank k-step that the partner needs.
   float gpart = 0.f;
   if constexpr (C::NRB > 0) {
-    if (graph && qvalid) {
 #pragma unroll
-      for (int f = 0; f < C::NRB; ++f)
+    for (int f = 0; f < C::NRB; ++f) {
+      u32x2 rv[4];
+      if constexpr (RQ_COPY) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x16& a = acc[C::NDB + f];
-          const u32x2 rv = rq_epi[f][g];
-          if (f * 32 + 8 * g + 4 * hl < p.R)
-            gpart += bf16_lo(rv[0]) * a[4 * g] + bf16_hi(rv[0]) * a[4 * g + 1] +
-                     bf16_lo(rv[1]) * a[4 * g + 2] + bf16_hi(rv[1]) * a[4 * g + 3];
+        for (int g = 0; g < 4; ++g) rv[g] = rq_epi[f][g];
+      } else {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const u32x4 q = as_u32x4(qreg[C::KSD + 2 * f + t]);
+          const uint32_t x0 = __shfl_xor(hl ? q[0] : q[2], 32);
+          const uint32_t x1 = __shfl_xor(hl ? q[1] : q[3], 32);
+          // this lane's half of features 32f + 16t + 8hl .. +7 that it
+          // keeps (lower for hl = 0, upper for hl = 1), and the partner's
+          const u32x2 own = hl ? u32x2{q[2], q[3]} : u32x2{q[0], q[1]};
+          const u32x2 got = u32x2{x0, x1};
+          rv[2 * t] = hl ? got : own;      // g = 2t:     features 16t + 4hl .. +3
+          rv[2 * t + 1] = hl ? own : got;  // g = 2t + 1: features 16t + 8 + 4hl .. +3
         }
+      }
+      if (graph && qvalid) {
+        const f32x16& a = acc[C::NDB + f];
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          if (f * 32 + 8 * g + 4 * hl < p.R)
+            gpart += bf16_lo(rv[g][0]) * a[4 * g] + bf16_hi(rv[g][0]) * a[4 * g + 1] +
+                     bf16_lo(rv[g][1]) * a[4 * g + 2] + bf16_hi(rv[g][1]) * a[4 * g + 3];
+      }
     }
   }
   // Epilogue: the ring is idle once every wave has left the loop, so each
@@ -376,8 +404,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   }
 }
 
-// WAVES: waves per SIMD the register budget is cut for (d128/r64 needs more
-// registers than two waves allow without spilling).
+// WAVES: waves per SIMD the register budget is cut for.
 #define FNA2_DQ_KERNEL(D, RPL, WAVES)                                                   \
   __global__ __launch_bounds__(256, WAVES) void dq_kernel_d##D##_r##RPL(const BwdParams P) { \
     dq_body<D, RPL>(P);                                                                 \
@@ -387,7 +414,7 @@ FNA2_DQ_KERNEL(64, 32, 3)
 FNA2_DQ_KERNEL(64, 64, 2)
 FNA2_DQ_KERNEL(128, 0, 2)
 FNA2_DQ_KERNEL(128, 32, 2)
-FNA2_DQ_KERNEL(128, 64, 1)
+FNA2_DQ_KERNEL(128, 64, 2)
 #undef FNA2_DQ_KERNEL
 
 }  // namespace
