@@ -518,18 +518,24 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     uint8_t* obuf = epi + kw * RowStage<D>::BYTES;
     auto write_rows = [&](const KvItem& x, const f32x16* acc, float sc, bool zero,
                           const TView& out) {
+      // (The lane index is made opaque so that the compiler forms the
+      // staging addresses here instead of hoisting them out of the item
+      // loop, where they would hold registers throughout.)
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int row = ln & 31, half = ln >> 5;
 #pragma unroll
       for (int d = 0; d < C::NDB; ++d)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const f32x16& a = acc[d];
-          RowStage<D>::put4(obuf, l32, d * 32 + 8 * q + 4 * hl, zero ? 0.f : sc * a[4 * q],
+          RowStage<D>::put4(obuf, row, d * 32 + 8 * q + 4 * half, zero ? 0.f : sc * a[4 * q],
                             zero ? 0.f : sc * a[4 * q + 1], zero ? 0.f : sc * a[4 * q + 2],
                             zero ? 0.f : sc * a[4 * q + 3]);
         }
       const int k0 = x.k0t + kw * 32;
       uint16_t* base = seq_base<uint16_t>(out, p, x.b, x.e.k0, x.kvh) + (int64_t)k0 * out.ss;
-      RowStage<D>::store(obuf, base, out.ss, x.e.lk - k0, D / 8, lane);
+      RowStage<D>::store(obuf, base, out.ss, x.e.lk - k0, D / 8, ln);
     };
     auto write_dkdv = [&](const KvItem& x, bool zero) {
       const ParamsPtr pp = params_here();
