@@ -301,7 +301,10 @@ def _fna2_forward_varlen(
     cu_k = cu_seqlens_k.to(device=q.device, dtype=torch.int32).contiguous()
     gs = _gs32(graph_scale) if H_G else None
     out = torch.empty_like(q)
-    lse = torch.empty(total_q, H, device=q.device, dtype=torch.float32)
+    # [T, H] as the reference returns it, viewing head-major memory: a
+    # workgroup's 128 rows of one head are then one contiguous run (row-major
+    # [T, H] put each 4-byte value in its own 64-byte segment).
+    lse = torch.empty(H, total_q, device=q.device, dtype=torch.float32).t()
     prob = _problem(True, N, max_seqlen_q, max_seqlen_k, total_q, total_k, H, H_KV, H_G, D, R,
                     is_causal, softmax_scale, cu_q, cu_k)
     _run_fwd(prob, q, k, v, r_q if H_G else None, r_k if H_G else None, gs, out, lse, _view3,
@@ -367,7 +370,8 @@ def _fna2_backward_varlen(
     cu_q = cu_seqlens_q.to(device=q.device, dtype=torch.int32).contiguous()
     cu_k = cu_seqlens_k.to(device=q.device, dtype=torch.int32).contiguous()
     gs = _gs32(graph_scale) if H_G else None
-    lse = lse.contiguous()
+    # (lse is read through its strides: the forward's head-major view or a
+    # row-major [T, H] alike)
     # [T, H] view of head-major memory: the dK/dV kernel reads a head's rows
     delta = torch.empty(H, total_q, device=q.device, dtype=torch.float32).t()
     dq, dk, dv, dr_q, dr_k = _grads_like(q, k, v, r_q, r_k, H_G)

@@ -9,8 +9,9 @@ kernels through the C ABI) are registered with ``torch.library.custom_op``:
 * ``fna2::fwd(q, k, v, r_q, r_k, graph_scale, softmax_scale, is_causal,
   cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k) -> (out, lse,
   plan)``: ``out`` has q's shape, dtype and strides; ``lse`` is fp32
-  ``[B, H, S]`` (dense) or ``[T, H]`` (varlen); ``plan`` is the uint8 buffer
-  of the varlen tile lists the backward reuses (empty in dense mode);
+  ``[B, H, S]`` (dense) or ``[T, H]`` (varlen, a view of head-major memory);
+  ``plan`` is the uint8 buffer of the varlen tile lists the backward reuses
+  (empty in dense mode);
 * ``fna2::bwd(dout, q, k, v, r_q, r_k, graph_scale, out, lse, plan, ...) ->
   (dq, dk, dv, dr_q, dr_k, d_graph_scale)``, absent gradients (no graph
   heads) as empty tensors;
@@ -92,7 +93,7 @@ def _fna2_fwd_fake(q, k, v, r_q, r_k, graph_scale, softmax_scale, is_causal, cu_
         lse = q.new_empty((q.shape[0], q.shape[1], q.shape[2]), dtype=torch.float32)
         plan = q.new_empty((0,), dtype=torch.uint8)
     else:
-        lse = q.new_empty((q.shape[0], q.shape[1]), dtype=torch.float32)
+        lse = q.new_empty((q.shape[1], q.shape[0]), dtype=torch.float32).t()  # head-major
         nbytes = plan_nbytes(q.shape[0], k.shape[0], cu_seqlens_q.shape[0] - 1)
         plan = q.new_empty((nbytes,), dtype=torch.uint8)
     return out, lse, plan
