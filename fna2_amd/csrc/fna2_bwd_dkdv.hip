@@ -69,6 +69,14 @@ struct KvCfg {
   static constexpr int N_KV = 2 * KSD + KSR;  // stationary-row loads of an item
   using DmaD = Dma<BM, CD, NP>;
   using DmaR = Dma<BM, CR, NP>;
+  // K and Rk tiles of the next (item, head) in LDS, DMA'd by the consumer
+  // waves, where the LDS holds them next to the ring (not at d = 128 with
+  // rank 64).
+  static constexpr int KRK = BN * CD * 16;
+  static constexpr int KRR = RPL > 0 ? BN * CR * 16 : 0;
+  static constexpr bool KR = 4 * STAGE + 2 * PDS + KRK + KRR <= 160 * 1024;
+  using DmaKK = Dma<BN, CD, NP>;
+  using DmaKR = Dma<BN, CR, NP>;
   // VMEM instructions every producer wave issues per block (Q, dO, rank
   // operand, one -LSE log2(e) / delta row), the same for every wave.
   static constexpr int NB = 2 * DmaD::PER_WAVE + (RPL > 0 ? DmaR::PER_WAVE : 0) + 1;
@@ -131,7 +139,8 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
   __shared__ __attribute__((aligned(1024))) uint8_t st3[C::STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t pd0[C::PDS];
   __shared__ __attribute__((aligned(1024))) uint8_t pd1[C::PDS];
-  __shared__ __attribute__((aligned(16))) uint8_t epi[C::NP * RowStage<D>::BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t krk[C::KR ? C::KRK : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t krr[C::KR && RPL > 0 ? C::KRR : 16];
   const Problem& p = P.p;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = uni(tid >> 6);
@@ -193,6 +202,12 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     next_item(c, on_zero);
   };
   auto no_zero = [](const KvItem&) {};
+  // The first block of the (item, head) after the cursor's (lookahead only).
+  auto next_seg = [&](KvCursor c) {
+    c.qi = 0;
+    if (++c.hi >= p.group) next_item(c, no_zero);
+    return c;
+  };
   // Whether this wave's 32 keys meet block qi of the cursor's item.
   auto block_active = [&](const KvCursor& c) {
     const int wk0 = c.it.k0t + kw * 32;
@@ -266,31 +281,61 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     for (int s = 0; s < C::KSD + C::KSR; ++s) kreg[s] = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int s = 0; s < C::KSD; ++s) vreg[s] = u32x4{0u, 0u, 0u, 0u};
-    auto load_rows = [&](const KvItem& x, int h) {
+    auto load_k = [&](const KvItem& x, int h, bool skip) {
       const ParamsPtr pp = params_here();
-      const TView vk = view_of(&pp->k), vv = view_of(&pp->v), vr = view_of(&pp->rk);
+      const TView vk = view_of(&pp->k), vr = view_of(&pp->rk);
       const uint32_t krows = (uint32_t)max(min(C::BN, x.e.lk - x.k0t), 0);
-      const uint32_t krb = (uint32_t)vk.ss * 2u, vrb = (uint32_t)vv.ss * 2u;
+      const uint32_t krb = (uint32_t)vk.ss * 2u;
       const uint32_t rrb = (uint32_t)vr.ss * 2u;
       const bool graph = h < p.H_G;
       const uint16_t* kb = seq_base<const uint16_t>(vk, p, x.b, x.e.k0, x.kvh);
-      const uint16_t* vb = seq_base<const uint16_t>(vv, p, x.b, x.e.k0, x.kvh);
       const uint16_t* rkb = graph ? seq_base<const uint16_t>(vr, p, x.b, x.e.k0, h) : kb;
       const u32x4 rk = rsrc_words(kb + (int64_t)x.k0t * vk.ss, krows * krb);
-      const u32x4 rv = rsrc_words(vb + (int64_t)x.k0t * vv.ss, krows * vrb);
       const u32x4 rr = rsrc_words(rkb + (int64_t)x.k0t * vr.ss, graph ? krows * rrb : 0u);
-      const uint32_t ko = (uint32_t)krow * krb + 16u * hl;
-      const uint32_t vo = (uint32_t)krow * vrb + 16u * hl;
+      // skip: every offset out of range (the buffer unit returns zeros
+      // without touching memory), so that this is one load site whichever
+      // way the rows come
+      const uint32_t ko = skip ? kOOB : (uint32_t)krow * krb + 16u * hl;
       const uint32_t ro = (uint32_t)krow * rrb + 16u * hl;
-      static_for<C::KSD>([&](auto s) {
-        load16_inplace<32 * decltype(s)::value>(kreg[s], rk, ko);
-        load16_inplace<32 * decltype(s)::value>(vreg[s], rv, vo);
-      });
+      static_for<C::KSD>([&](auto s) { load16_inplace<32 * decltype(s)::value>(kreg[s], rk, ko); });
       static_for<C::KSR>([&](auto s) {
-        const bool in = (2 * decltype(s)::value + hl) * 8 < p.R;
+        const bool in = !skip && (2 * decltype(s)::value + hl) * 8 < p.R;
         load16_inplace<32 * decltype(s)::value>(kreg[C::KSD + s], rr, in ? ro : kOOB);
       });
     };
+    auto load_v = [&](const KvItem& x) {
+      const ParamsPtr pp = params_here();
+      const TView vv = view_of(&pp->v);
+      const uint32_t krows = (uint32_t)max(min(C::BN, x.e.lk - x.k0t), 0);
+      const uint32_t vrb = (uint32_t)vv.ss * 2u;
+      const uint16_t* vb = seq_base<const uint16_t>(vv, p, x.b, x.e.k0, x.kvh);
+      const u32x4 rv = rsrc_words(vb + (int64_t)x.k0t * vv.ss, krows * vrb);
+      const uint32_t vo = (uint32_t)krow * vrb + 16u * hl;
+      static_for<C::KSD>([&](auto s) { load16_inplace<32 * decltype(s)::value>(vreg[s], rv, vo); });
+    };
+    // K | Rk rows of this wave's keys from the LDS tiles the consumers filled
+    // (the row-read pattern of the tiles: chunk 2s + lane / 32 of row
+    // kw * 32 + lane % 32).  In place, as every other write of these
+    // registers, so that the compiler keeps them where the in-place global
+    // loads put them; the explicit wait replaces the one it does not insert.
+    auto read_kr = [&]() {
+      const uint32_t kb0 = lds_addr(krk) + (uint32_t)(kw * 32 * 64 + rdl.off[0]);
+      const uint32_t kb1 = lds_addr(krk) + (uint32_t)(kw * 32 * 64 + rdl.off[1]);
+      static_for<C::KSD>([&](auto s) {
+        constexpr int S = decltype(s)::value;
+        ds_read16_inplace<(S >> 1) * C::BN * 64>(kreg[S], (S & 1) ? kb1 : kb0);
+      });
+      if constexpr (C::KSR > 0) {
+        const uint32_t rb0 = lds_addr(krr) + (uint32_t)(kw * 32 * 64 + rdl.off[0]);
+        const uint32_t rb1 = lds_addr(krr) + (uint32_t)(kw * 32 * 64 + rdl.off[1]);
+        static_for<C::KSR>([&](auto s) {
+          constexpr int S = decltype(s)::value;
+          ds_read16_inplace<(S >> 1) * C::BN * 64>(kreg[C::KSD + S], (S & 1) ? rb1 : rb0);
+        });
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    };
+    bool kr_in = false;  // the current (item, head)'s K | Rk wait in LDS
     // The streamed Q tile is raw, so the factor a in {1, -1, 0} of the
     // augmented operand goes on K (exact): Q (a K)^T = (a Q) K^T.
     const uint32_t kxor = p.qa < 0.f ? 0x80008000u : 0u;
@@ -419,7 +464,10 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     start(pc, no_zero);
     KvCursor ic = pc;  // the block whose tiles are issued next (two ahead)
     setup(ic);
-    if (!pc.done) load_rows(pc.it, pc.it.kvh * p.group + pc.hi);
+    if (!pc.done) {
+      load_k(pc.it, pc.it.kvh * p.group + pc.hi, false);
+      load_v(pc.it);
+    }
     issue(ic, st0);
     if (!ic.done) {
       advance(ic, no_zero);
@@ -440,6 +488,10 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       ring_barrier<C::NB>();
       if (pc.done) return;
       if (pc.qi == 0) {  // rows loaded by the previous block (or above)
+        if constexpr (C::KR) {
+          if (kr_in) read_kr();
+          kr_in = false;
+        }
         sign_k();
         bhp = head_scale(pc);
       }
@@ -451,7 +503,17 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       __builtin_amdgcn_sched_barrier(0);
       if (act) scores(pc, cur, sacc, dpacc, lsr);
       __builtin_amdgcn_sched_barrier(0);
-      if (!nx.done && nx.qi == 0) load_rows(nx.it, nx.it.kvh * p.group + nx.hi);
+      if (!nx.done && nx.qi == 0) {
+        // The next (item, head)'s rows: after an (item, head) of two or more
+        // blocks the consumers have DMA'd its K | Rk into LDS, and only V is
+        // loaded here.
+        // (One load site for each: branches around in-place loads of the
+        // same registers made the compiler move them while in flight.)
+        const bool from_lds = C::KR && pc.it.nqb >= 2;
+        load_k(nx.it, nx.it.kvh * p.group + nx.hi, from_lds);
+        load_v(nx.it);
+        kr_in = from_lds;
+      }
       __builtin_amdgcn_sched_barrier(0);
       if (act) softmax(pc, pd, sacc, dpacc, lsr);
       __builtin_amdgcn_sched_barrier(0);
@@ -513,39 +575,73 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
         }
       }
     };
-    // dK = a c acc_D and dV: each wave stages its 32 rows through its own LDS
-    // buffer so that a store instruction writes whole rows.
-    uint8_t* obuf = epi + kw * RowStage<D>::BYTES;
+    // dK = a c acc_D and dV: each wave stages its 32 rows in its own 4 KB of
+    // the P / dS buffer it has just consumed (free until the next barrier),
+    // 64 features at a time, so that a store instruction writes whole
+    // 128-byte row pieces.
+    using HS = RowStage<64>;
+    static_assert(HS::BYTES == C::PW, "a half-row stage fills a wave's P / dS slot");
     auto write_rows = [&](const KvItem& x, const f32x16* acc, float sc, bool zero,
-                          const TView& out) {
+                          const TView& out, uint8_t* sbuf) {
       // (The lane index is made opaque so that the compiler forms the
       // staging addresses here instead of hoisting them out of the item
       // loop, where they would hold registers throughout.)
       int ln = lane;
       asm volatile("" : "+v"(ln));
       const int row = ln & 31, half = ln >> 5;
-#pragma unroll
-      for (int d = 0; d < C::NDB; ++d)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const f32x16& a = acc[d];
-          RowStage<D>::put4(obuf, row, d * 32 + 8 * q + 4 * half, zero ? 0.f : sc * a[4 * q],
-                            zero ? 0.f : sc * a[4 * q + 1], zero ? 0.f : sc * a[4 * q + 2],
-                            zero ? 0.f : sc * a[4 * q + 3]);
-        }
       const int k0 = x.k0t + kw * 32;
       uint16_t* base = seq_base<uint16_t>(out, p, x.b, x.e.k0, x.kvh) + (int64_t)k0 * out.ss;
-      RowStage<D>::store(obuf, base, out.ss, x.e.lk - k0, D / 8, ln);
+#pragma unroll
+      for (int hp = 0; hp < D / 64; ++hp) {
+#pragma unroll
+        for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x16& a = acc[2 * hp + dd];
+            HS::put4(sbuf, row, dd * 32 + 8 * q + 4 * half, zero ? 0.f : sc * a[4 * q],
+                     zero ? 0.f : sc * a[4 * q + 1], zero ? 0.f : sc * a[4 * q + 2],
+                     zero ? 0.f : sc * a[4 * q + 3]);
+          }
+        HS::store(sbuf, base + hp * 64, out.ss, x.e.lk - k0, HS::CPR, ln);
+      }
     };
+    uint8_t* sbuf = pd0 + kw * C::PW;  // staging slot (pd0 is free before the first barrier)
     auto write_dkdv = [&](const KvItem& x, bool zero) {
       const ParamsPtr pp = params_here();
-      write_rows(x, dkacc, p.qa * p.c, zero, view_of(&pp->dk));
-      write_rows(x, dvacc, 1.f, zero, view_of(&pp->dv));
+      write_rows(x, dkacc, p.qa * p.c, zero, view_of(&pp->dk), sbuf);
+      write_rows(x, dvacc, 1.f, zero, view_of(&pp->dv), sbuf);
     };
     auto on_zero = [&](const KvItem& x) {
       write_dkdv(x, true);
       for (int hi = 0; hi < p.group; ++hi) write_drk(x, x.kvh * p.group + hi, true);
     };
+
+    // K | Rk of the (item, head) after the one whose first block is being
+    // consumed, DMA'd into LDS for the producers' next switch.  This wave's
+    // share of the two tiles; rows past the sequence and rank chunks past R
+    // read as zeros.
+    typename C::DmaKK dkk;
+    typename C::DmaKR dkr;
+    const uint32_t kkb = (uint32_t)P.k.ss * 2u, krb2 = (uint32_t)P.rk.ss * 2u;
+    if constexpr (C::KR) {
+      dkk.init_fixed(kw, lane, kkb, C::CD);
+      if constexpr (RPL > 0) dkr.init_fixed(kw, lane, krb2, p.R / 8);
+    }
+    auto issue_kr = [&](const KvItem& x, int h) {
+      const ParamsPtr pp = params_here();
+      const TView vk = view_of(&pp->k), vr = view_of(&pp->rk);
+      const uint32_t krows = (uint32_t)max(min(C::BN, x.e.lk - x.k0t), 0);
+      const uint16_t* kb =
+          seq_base<const uint16_t>(vk, p, x.b, x.e.k0, x.kvh) + (int64_t)x.k0t * vk.ss;
+      dkk.issue_fixed(rsrc_words(kb, krows * kkb), krk, kw, 0u);
+      if constexpr (RPL > 0) {
+        const bool graph = h < p.H_G;
+        const uint16_t* rb =
+            graph ? seq_base<const uint16_t>(vr, p, x.b, x.e.k0, h) + (int64_t)x.k0t * vr.ss : kb;
+        dkr.issue_fixed(rsrc_words(rb, graph ? krows * krb2 : 0u), krr, kw, 0u);
+      }
+    };
+    bool kr_issued = false;
 
     // (acc_R of a vanilla head is built from zero tiles and never stored.)
     auto consume = [&](const uint8_t* cur, const uint8_t* pd) {
@@ -585,7 +681,16 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     // Step t consumes block t - 1 (nothing at t = 0).  The barrier does not
     // wait for the consumers' own stores.
     bool first = true;
-    auto step = [&](const uint8_t* cur, const uint8_t* pd) {
+    auto step = [&](const uint8_t* cur, uint8_t* pd) {
+      if constexpr (C::KR) {
+        // The producers switch to the next (item, head) at this step and
+        // read its K | Rk from LDS after the barrier: this wave's DMA of it
+        // must be complete.
+        if (kr_issued && !first && !cc.done && cc.qi + 1 == cc.it.nqb) {
+          __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+          kr_issued = false;
+        }
+      }
       ring_barrier<63>();
       if (first) {
         first = false;
@@ -593,10 +698,22 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       }
       if (cc.done) return;
       if (block_active(cc)) consume(cur, pd);
+      if constexpr (C::KR) {
+        // After the first block of an (item, head) of two or more blocks
+        // (the producers read its K | Rk before this step's barrier).
+        if (cc.qi == 0 && cc.it.nqb >= 2) {
+          const KvCursor ny = next_seg(cc);
+          if (!ny.done) {
+            issue_kr(ny.it, ny.it.kvh * p.group + ny.hi);
+            kr_issued = true;
+          }
+        }
+      }
       if (cc.qi + 1 < cc.it.nqb) {
         ++cc.qi;
         return;
       }
+      sbuf = pd + kw * C::PW;
       __builtin_amdgcn_sched_barrier(0);
       const KvItem x = cc.it;
       const bool last_head = cc.hi + 1 == p.group;
@@ -613,6 +730,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       advance(cc, on_zero);
     };
     // Stage and P/dS buffer of block t - 1: st[(t + 3) % 4], pd[(t + 1) % 2].
+    // (The epilogue and zero items of step t stage in that P/dS buffer.)
     for (;;) {
       step(st3, pd1);
       if (cc.done) break;

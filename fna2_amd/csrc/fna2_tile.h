@@ -101,6 +101,14 @@ __device__ __forceinline__ void load16_inplace(u32x4& dst, const u32x4& rs, uint
                : "v"(voffset), "s"(rs), "i"(IMM));
 }
 
+// 16-byte LDS read at byte address lds + IMM into the registers that hold
+// `dst`, in place (the caller waits: lgkmcnt).
+template <int IMM>
+__device__ __forceinline__ void ds_read16_inplace(u32x4& dst, uint32_t lds) {
+  static_assert(IMM >= 0 && IMM < 65536, "ds offset field");
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "+v"(dst) : "v"(lds), "i"(IMM));
+}
+
 // 2-bit chunk swizzle of a row (row bits 1..3).
 __device__ __forceinline__ int swz4(int r) {
   return ((((r >> 1) ^ (r >> 3)) & 1) << 1) | ((r >> 2) & 1);
