@@ -20,7 +20,8 @@
 //       dV^T  += dO^T P                A operand: dO^T by transpose reads
 //       acc^T += [Q | Rq]^T dS         A operand: the same tiles transposed
 //     and at the end of an item writes dK = a c acc_D, dRk = graph_scale[h]
-//     acc_R (= graph_scale dS^T Rq) and dV.
+//     acc_R (= graph_scale dS^T Rq) and dV straight from the accumulators
+//     (one lane exchange per register pair makes 16-byte row pieces).
 // A producer's softmax arithmetic thus overlaps its SIMD partner's MFMAs,
 // and neither role needs more than half of the SIMD's registers.  dK and dV
 // accumulate over the whole GQA group in fp32: no atomics.
@@ -35,7 +36,9 @@
 // the producers) through a four-stage ring that runs two blocks ahead of the
 // producers, across item boundaries; the consumers read a stage one block
 // later.  The last block of an (item, head) loads the rows of the next one
-// into the registers its MFMAs have just read.  Both roles meet at one
+// into the registers its MFMAs have just read: V from memory, K | Rk from
+// LDS tiles that the consumers DMA'd during the current one (where the LDS
+// has room for them).  Both roles meet at one
 // barrier per block.  The stages are separate LDS objects and the loops are
 // unrolled by four so that the compiler can prove that reads and in-flight
 // DMA never alias.
@@ -552,64 +555,61 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     for (int i = 0; i < C::NDB + C::NRB; ++i) dkacc[i] = f32x16{};
 
     // dRk of head h = graph_scale[h] acc_R (zero: an item no query block sees).
+    // Lane (key l32, half hl) holds features 32 t + 8 i + 4 hl + e of its key
+    // in accumulator tile t; one exchange between the lane halves per
+    // register pair (i = 2 u, 2 u + 1) gives each lane 8 consecutive
+    // features: 32 t + 16 u + 8 hl .. +7, in the returned order.
+    auto swap8 = [&](const f32x16& a, float sc, bool zero, int u) {
+      auto pk = [&](int v) { return zero ? 0u : pack_bf16(sc * a[v], sc * a[v + 1]); };
+      const auto lo = __builtin_amdgcn_permlane32_swap(pk(8 * u), pk(8 * u + 4), false, false);
+      const auto hi = __builtin_amdgcn_permlane32_swap(pk(8 * u + 2), pk(8 * u + 6), false, false);
+      return u32x4{lo[0], hi[0], lo[1], hi[1]};
+    };
     auto write_drk = [&](const KvItem& x, int h, bool zero) {
       if constexpr (C::NRB > 0) {
-        const int key = x.k0t + krow;
-        if (h < p.H_G && key < x.e.lk) {
+        if (h < p.H_G) {
           const float sr = zero ? 0.f : *const_space(params_here()->gs + h);
-          const TView vd = view_of(&params_here()->drk);
-          uint16_t* rrow = seq_base<uint16_t>(vd, p, x.b, x.e.k0, h) + (int64_t)key * vd.ss;
+          u32x4 w[C::NRB][2];
 #pragma unroll
           for (int f = 0; f < C::NRB; ++f)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int rf = f * 32 + 8 * q + 4 * hl;
-              if (rf < p.R) {
-                const f32x16& a = dkacc[C::NDB + f];
-                u32x2 val;
-                val[0] = zero ? 0u : pack_bf16(sr * a[4 * q], sr * a[4 * q + 1]);
-                val[1] = zero ? 0u : pack_bf16(sr * a[4 * q + 2], sr * a[4 * q + 3]);
-                *(u32x2*)(rrow + rf) = val;
-              }
-            }
+            for (int u = 0; u < 2; ++u) w[f][u] = swap8(dkacc[C::NDB + f], sr, zero, u);
+          const int key = x.k0t + krow;
+          if (key < x.e.lk) {
+            const TView vd = view_of(&params_here()->drk);
+            uint16_t* rp = seq_base<uint16_t>(vd, p, x.b, x.e.k0, h) + (int64_t)key * vd.ss + 8 * hl;
+#pragma unroll
+            for (int f = 0; f < C::NRB; ++f)
+#pragma unroll
+              for (int u = 0; u < 2; ++u)
+                if (32 * f + 16 * u + 8 * hl < p.R) *(u32x4*)(rp + 32 * f + 16 * u) = w[f][u];
+          }
         }
       }
     };
-    // dK = a c acc_D and dV: each wave stages its 32 rows in its own 4 KB of
-    // the P / dS buffer it has just consumed (free until the next barrier),
-    // 64 features at a time, so that a store instruction writes whole
-    // 128-byte row pieces.
-    using HS = RowStage<64>;
-    static_assert(HS::BYTES == C::PW, "a half-row stage fills a wave's P / dS slot");
+    // dK = a c acc_D and dV, 16 bytes per lane straight from the
+    // accumulators: a store writes 32 contiguous bytes of each of the wave's
+    // 32 rows.
     auto write_rows = [&](const KvItem& x, const f32x16* acc, float sc, bool zero,
-                          const TView& out, uint8_t* sbuf) {
-      // (The lane index is made opaque so that the compiler forms the
-      // staging addresses here instead of hoisting them out of the item
-      // loop, where they would hold registers throughout.)
-      int ln = lane;
-      asm volatile("" : "+v"(ln));
-      const int row = ln & 31, half = ln >> 5;
-      const int k0 = x.k0t + kw * 32;
-      uint16_t* base = seq_base<uint16_t>(out, p, x.b, x.e.k0, x.kvh) + (int64_t)k0 * out.ss;
+                          const TView& out) {
+      u32x4 w[C::NDB][2];
 #pragma unroll
-      for (int hp = 0; hp < D / 64; ++hp) {
+      for (int t = 0; t < C::NDB; ++t)
 #pragma unroll
-        for (int dd = 0; dd < 2; ++dd)
+        for (int u = 0; u < 2; ++u) w[t][u] = swap8(acc[t], sc, zero, u);
+      const int key = x.k0t + krow;
+      if (key < x.e.lk) {
+        uint16_t* rp = seq_base<uint16_t>(out, p, x.b, x.e.k0, x.kvh) + (int64_t)key * out.ss + 8 * hl;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const f32x16& a = acc[2 * hp + dd];
-            HS::put4(sbuf, row, dd * 32 + 8 * q + 4 * half, zero ? 0.f : sc * a[4 * q],
-                     zero ? 0.f : sc * a[4 * q + 1], zero ? 0.f : sc * a[4 * q + 2],
-                     zero ? 0.f : sc * a[4 * q + 3]);
-          }
-        HS::store(sbuf, base + hp * 64, out.ss, x.e.lk - k0, HS::CPR, ln);
+        for (int t = 0; t < C::NDB; ++t)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) *(u32x4*)(rp + 32 * t + 16 * u) = w[t][u];
       }
     };
-    uint8_t* sbuf = pd0 + kw * C::PW;  // staging slot (pd0 is free before the first barrier)
     auto write_dkdv = [&](const KvItem& x, bool zero) {
       const ParamsPtr pp = params_here();
-      write_rows(x, dkacc, p.qa * p.c, zero, view_of(&pp->dk), sbuf);
-      write_rows(x, dvacc, 1.f, zero, view_of(&pp->dv), sbuf);
+      write_rows(x, dkacc, p.qa * p.c, zero, view_of(&pp->dk));
+      write_rows(x, dvacc, 1.f, zero, view_of(&pp->dv));
     };
     auto on_zero = [&](const KvItem& x) {
       write_dkdv(x, true);
@@ -713,7 +713,6 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
         ++cc.qi;
         return;
       }
-      sbuf = pd + kw * C::PW;
       __builtin_amdgcn_sched_barrier(0);
       const KvItem x = cc.it;
       const bool last_head = cc.hi + 1 == p.group;
@@ -730,7 +729,6 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       advance(cc, on_zero);
     };
     // Stage and P/dS buffer of block t - 1: st[(t + 3) % 4], pd[(t + 1) % 2].
-    // (The epilogue and zero items of step t stage in that P/dS buffer.)
     for (;;) {
       step(st3, pd1);
       if (cc.done) break;
