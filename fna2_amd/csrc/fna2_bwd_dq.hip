@@ -86,6 +86,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   const int tix = blockIdx.x / p.H;
   int b, qt;
   SeqExt e;
+  int slot = tix;  // the tile's d_gs partial rows (list order in dense mode is fixed)
   if (P.tiles_q) {
     const int nt = min(uni(*const_space(P.n_tiles_q)), P.q_tiles);
     if (tix >= nt) {
@@ -93,6 +94,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
       return;
     }
     tile_decode(P.tiles_q, tix, b, qt, e);
+    slot = tile_slot(P.tiles_q, tix);
   } else {
     const int nqt = cdiv(p.sq, C::BM);
     b = tix % p.nseq;
@@ -399,7 +401,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
     if (graph) {
 #pragma unroll
       for (int off = 32; off > 0; off >>= 1) gpart += __shfl_xor(gpart, off);
-      if (lane == 0) P.dgs_partial[((int64_t)tix * 4 + wv) * p.H_G + h] = gpart;
+      if (lane == 0 && slot < P.q_tiles) P.dgs_partial[((int64_t)slot * 4 + wv) * p.H_G + h] = gpart;
     }
   }
 }

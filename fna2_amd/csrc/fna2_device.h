@@ -133,9 +133,16 @@ __device__ __forceinline__ SeqExt seq_ext_uniform(const Problem& p, int b) {
 
 // A varlen work tile: sequence b, tile t within it and the sequence's clamped
 // extents, so that a kernel decodes a tile with one 32-byte scalar load.
+// slot: the tile's position in (sequence, tile) order, whatever order the
+// list holds it in (sums over tiles index by it, so they do not depend on
+// the list's order).
 struct __attribute__((aligned(32))) TileRec {
-  int b, t, q0, lq, k0, lk, pad0, pad1;
+  int b, t, q0, lq, k0, lk, slot, pad;
 };
+
+__device__ __forceinline__ int tile_slot(const TileRec* __restrict__ tiles, int tix) {
+  return uni((const_space(tiles) + uni(tix))->slot);
+}
 
 __device__ __forceinline__ void tile_decode(const TileRec* __restrict__ tiles, int tix, int& b,
                                             int& t, SeqExt& e) {

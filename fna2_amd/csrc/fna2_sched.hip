@@ -142,25 +142,49 @@ __global__ __launch_bounds__(kThreads) void build_tiles_kernel(Problem p, TileLi
     *count = min(total, cap);
   }
 
-  // Pass 2: scatter (the order inside a bucket is irrelevant: tiles are
-  // independent and each writes its own outputs).  A grouped sequence
-  // claims a run of positions and writes its tiles most work first: under
-  // the causal mask the last query tile and the first key tile.
+  // Pass 2: scatter.  The order of the claims inside a bucket varies from
+  // run to run; no result does: tiles are independent, each writes its own
+  // outputs, and each carries its slot (position in (sequence, tile) order:
+  // an exclusive scan of the tile counts over the sequences), by which sums
+  // over tiles are indexed.  A grouped sequence claims a run of positions
+  // and writes its tiles most work first: under the causal mask the last
+  // query tile and the first key tile.
   const bool reverse = spec.kind == 0 && p.causal;
-  for (int b = tid; b < p.nseq; b += kThreads) {
-    const SeqExt e = seq_ext(p, b);
-    const int n = tile_count(e, spec);
+  int carry = 0;  // tiles of the sequences before this chunk
+  for (int base = 0; base < p.nseq; base += kThreads) {
+    const int b = base + tid;
+    SeqExt e{};
+    int n = 0;
+    if (b < p.nseq) {
+      e = seq_ext(p, b);
+      n = max(tile_count(e, spec), 0);
+    }
+    int sc = n;  // wave-level inclusive scan of the counts
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(sc, off);
+      if (lane >= off) sc += y;
+    }
+    __syncthreads();  // the previous readers of warp_tot are done
+    if (lane == 63) warp_tot[wid] = sc;
+    __syncthreads();
+    int before = 0, chunk = 0;
+    for (int w = 0; w < kThreads / 64; ++w) {
+      if (w < wid) before += warp_tot[w];
+      chunk += warp_tot[w];
+    }
+    const int slot0 = carry + before + sc - n;
+    carry += chunk;
     if (n <= 0) continue;
     if (spec.group) {
       const int pos = atomicAdd(&hist[seq_bucket(e, n)], n);
       for (int i = 0; i < n; ++i) {
         const int t = reverse ? n - 1 - i : i;
-        if (pos + i < cap) tiles[pos + i] = TileRec{b, t, e.q0, e.lq, e.k0, e.lk, 0, 0};
+        if (pos + i < cap) tiles[pos + i] = TileRec{b, t, e.q0, e.lq, e.k0, e.lk, slot0 + t, 0};
       }
     } else {
       for (int t = 0; t < n; ++t) {
         const int pos = atomicAdd(&hist[tile_bucket(e, t)], 1);
-        if (pos < cap) tiles[pos] = TileRec{b, t, e.q0, e.lq, e.k0, e.lk, 0, 0};
+        if (pos < cap) tiles[pos] = TileRec{b, t, e.q0, e.lq, e.k0, e.lk, slot0 + t, 0};
       }
     }
   }

@@ -224,6 +224,32 @@ def test_deterministic(gpu):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("use_plan", [False, True])
+def test_deterministic_varlen_equal_lengths(gpu, use_plan):
+    """Many sequences of one length (c5's pattern: the list builder places
+    equal-work tiles in a different order on every run) and graph heads:
+    every output, d_graph_scale included, bit for bit the same over runs.
+    d_graph_scale sums per-tile partials, which are indexed by the tile's
+    (sequence, tile) slot rather than its list position."""
+    F = _fna2()
+    lengths = [48] * 200 + [700] + [16] * 60
+    (q, k, v, rq, rk, gs_, dout, cu_q, _) = H.make_varlen(lengths, 4, 64, 4, 4, 16, seed=41)
+    g = [t.to(gpu) for t in (q, k, v, rq, rk, gs_, dout, cu_q)]
+    mx, scale = max(lengths), 0.125
+    print(f"varlen determinism: {len(lengths)} sequences, plan {use_plan}", flush=True)
+    res = []
+    for _ in range(3):
+        plan = F._plan_for(g[0], g[1], g[3], g[7], g[7], mx, mx, False, scale) if use_plan else None
+        out, lse = F._fna2_forward_varlen(*g[:6], g[7], g[7], mx, mx, scale, False, plan=plan)
+        grads = F._fna2_backward_varlen(g[6], *g[:6], out, lse, g[7], g[7], mx, mx, scale, False,
+                                        plan=plan)
+        res.append([out.clone(), lse.clone(), *[t.clone() for t in grads]])
+    torch.cuda.synchronize()
+    for r in res[1:]:
+        for a, b in zip(r, res[0]):
+            assert torch.equal(a, b)
+
+
 def test_row0_equals_v0(gpu):
     """Causal row 0 attends only to key 0: O_0 = V_0 (to bf16 rounding)."""
     F = _fna2()
