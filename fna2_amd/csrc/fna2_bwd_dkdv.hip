@@ -53,9 +53,10 @@ template <int D, int RPL>
 struct KvCfg {
   static constexpr int NP = 4;       // producer waves (as many consumers)
   static constexpr int NW = 2 * NP;  // waves per workgroup
-  static constexpr int BN = kKvBN;   // keys per item
-  static constexpr int BM = kKvBM;   // queries per block
-  static_assert(BM == 32 && BN == 32 * NP, "one 32 x 32 MFMA block per wave");
+  static constexpr int KPW = kv_kpw(D, RPL);  // 32-key slices per wave
+  static constexpr int BN = kv_bn(D, RPL);    // keys per item
+  static constexpr int BM = kKvBM;            // queries per block
+  static_assert(BM == 32 && BN == 32 * NP * KPW, "32 x 32 MFMA blocks");
   static constexpr int CD = D / 8;
   static constexpr int CR = RPL > 0 ? RPL / 8 : 4;
   static constexpr int KSD = D / 16;
@@ -67,9 +68,8 @@ struct KvCfg {
   static constexpr int OB = BM * D * 2;
   static constexpr int LB = 2 * 256;  // -LSE log2(e), delta: one 64-lane dword DMA each
   static constexpr int STAGE = QB + RB + OB + LB;
-  static constexpr int PW = 4 * 1024;  // a producer's P and dS operands of one block
+  static constexpr int PW = KPW * 4 * 1024;  // a producer's P and dS operands of one block
   static constexpr int PDS = NP * PW;
-  static constexpr int N_KV = 2 * KSD + KSR;  // stationary-row loads of an item
   using DmaD = Dma<BM, CD, NP>;
   using DmaR = Dma<BM, CR, NP>;
   // K and Rk tiles of the next (item, head) in LDS, DMA'd by the consumer
@@ -85,21 +85,22 @@ struct KvCfg {
   static constexpr int NB = 2 * DmaD::PER_WAVE + (RPL > 0 ? DmaR::PER_WAVE : 0) + 1;
 };
 
-// Scheduling pattern for a region of n MFMAs that each consume `per` LDS
-// reads: `ahead` MFMAs' reads are issued first, then one MFMA and the reads
-// of a later one alternate.  This bounds the registers held by operands in
-// flight (the scheduler would otherwise hoist every read).
-template <int N, int PER, int AHEAD>
+// Scheduling pattern for a region of n operands, each `per` LDS reads that
+// feed `mper` MFMAs: `ahead` operands' reads are issued first, then the
+// MFMAs of one operand and the reads of a later one alternate.  This bounds
+// the registers held by operands in flight (the scheduler would otherwise
+// hoist every read).
+template <int N, int PER, int AHEAD, int MPER = 1>
 __device__ __forceinline__ void pipe_lds_mfma() {
 #pragma unroll
   for (int i = 0; i < AHEAD; ++i) __builtin_amdgcn_sched_group_barrier(0x100, PER, 0);
 #pragma unroll
   for (int i = 0; i < N - AHEAD; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, MPER, 0);
     __builtin_amdgcn_sched_group_barrier(0x100, PER, 0);
   }
 #pragma unroll
-  for (int i = 0; i < AHEAD; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+  for (int i = 0; i < AHEAD; ++i) __builtin_amdgcn_sched_group_barrier(0x008, MPER, 0);
 }
 
 // The kernel's parameter block, re-read where it is used: the pointer is
@@ -147,9 +148,10 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
   const Problem& p = P.p;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = uni(tid >> 6);
-  const int kw = wv & (C::NP - 1);  // key slice of this wave
+  const int kw = wv & (C::NP - 1);  // keys of this wave: 32-key slices kw KPW ..
   const int l32 = lane & 31, hl = lane >> 5;
-  const int krow = kw * 32 + l32;   // this lane's key within the item
+  // this lane's key within the item in the wave's slice j
+  auto krow_of = [&](int j) { return (kw * C::KPW + j) * 32 + l32; };
   const int G = gridDim.x, g = blockIdx.x;
   const int n_items =
       (P.tiles_k ? min(uni(*const_space(P.n_tiles_k)), P.k_tiles) : p.nseq * cdiv(p.sk, C::BN)) *
@@ -213,7 +215,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
   };
   // Whether this wave's 32 keys meet block qi of the cursor's item.
   auto block_active = [&](const KvCursor& c) {
-    const int wk0 = c.it.k0t + kw * 32;
+    const int wk0 = c.it.k0t + kw * 32 * C::KPW;
     const int qbase = (c.it.qb_lo + c.qi) * C::BM;
     return wk0 < c.it.e.lk && (!p.causal || qbase + C::BM - 1 >= wk0);
   };
@@ -279,11 +281,14 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     // out-of-range offset, so the buffer unit returns zeros: they are never
     // read from memory (past R lie the next head's rank or, for the last row
     // of the last graph head, the end of R_k's allocation).
-    u32x4 kreg[C::KSD + C::KSR], vreg[C::KSD];
+    u32x4 kreg[C::KPW][C::KSD + C::KSR], vreg[C::KPW][C::KSD];
 #pragma unroll
-    for (int s = 0; s < C::KSD + C::KSR; ++s) kreg[s] = u32x4{0u, 0u, 0u, 0u};
+    for (int j = 0; j < C::KPW; ++j) {
 #pragma unroll
-    for (int s = 0; s < C::KSD; ++s) vreg[s] = u32x4{0u, 0u, 0u, 0u};
+      for (int s = 0; s < C::KSD + C::KSR; ++s) kreg[j][s] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int s = 0; s < C::KSD; ++s) vreg[j][s] = u32x4{0u, 0u, 0u, 0u};
+    }
     auto load_k = [&](const KvItem& x, int h, bool skip) {
       const ParamsPtr pp = params_here();
       const TView vk = view_of(&pp->k), vr = view_of(&pp->rk);
@@ -298,13 +303,17 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       // skip: every offset out of range (the buffer unit returns zeros
       // without touching memory), so that this is one load site whichever
       // way the rows come
-      const uint32_t ko = skip ? kOOB : (uint32_t)krow * krb + 16u * hl;
-      const uint32_t ro = (uint32_t)krow * rrb + 16u * hl;
-      static_for<C::KSD>([&](auto s) { load16_inplace<32 * decltype(s)::value>(kreg[s], rk, ko); });
-      static_for<C::KSR>([&](auto s) {
-        const bool in = !skip && (2 * decltype(s)::value + hl) * 8 < p.R;
-        load16_inplace<32 * decltype(s)::value>(kreg[C::KSD + s], rr, in ? ro : kOOB);
-      });
+#pragma unroll
+      for (int j = 0; j < C::KPW; ++j) {
+        const uint32_t ko = skip ? kOOB : (uint32_t)krow_of(j) * krb + 16u * hl;
+        const uint32_t ro = (uint32_t)krow_of(j) * rrb + 16u * hl;
+        static_for<C::KSD>(
+            [&](auto s) { load16_inplace<32 * decltype(s)::value>(kreg[j][s], rk, ko); });
+        static_for<C::KSR>([&](auto s) {
+          const bool in = !skip && (2 * decltype(s)::value + hl) * 8 < p.R;
+          load16_inplace<32 * decltype(s)::value>(kreg[j][C::KSD + s], rr, in ? ro : kOOB);
+        });
+      }
     };
     auto load_v = [&](const KvItem& x) {
       const ParamsPtr pp = params_here();
@@ -313,8 +322,12 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       const uint32_t vrb = (uint32_t)vv.ss * 2u;
       const uint16_t* vb = seq_base<const uint16_t>(vv, p, x.b, x.e.k0, x.kvh);
       const u32x4 rv = rsrc_words(vb + (int64_t)x.k0t * vv.ss, krows * vrb);
-      const uint32_t vo = (uint32_t)krow * vrb + 16u * hl;
-      static_for<C::KSD>([&](auto s) { load16_inplace<32 * decltype(s)::value>(vreg[s], rv, vo); });
+#pragma unroll
+      for (int j = 0; j < C::KPW; ++j) {
+        const uint32_t vo = (uint32_t)krow_of(j) * vrb + 16u * hl;
+        static_for<C::KSD>(
+            [&](auto s) { load16_inplace<32 * decltype(s)::value>(vreg[j][s], rv, vo); });
+      }
     };
     // K | Rk rows of this wave's keys from the LDS tiles the consumers filled
     // (the row-read pattern of the tiles: chunk 2s + lane / 32 of row
@@ -322,19 +335,23 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     // registers, so that the compiler keeps them where the in-place global
     // loads put them; the explicit wait replaces the one it does not insert.
     auto read_kr = [&]() {
-      const uint32_t kb0 = lds_addr(krk) + (uint32_t)(kw * 32 * 64 + rdl.off[0]);
-      const uint32_t kb1 = lds_addr(krk) + (uint32_t)(kw * 32 * 64 + rdl.off[1]);
-      static_for<C::KSD>([&](auto s) {
-        constexpr int S = decltype(s)::value;
-        ds_read16_inplace<(S >> 1) * C::BN * 64>(kreg[S], (S & 1) ? kb1 : kb0);
-      });
-      if constexpr (C::KSR > 0) {
-        const uint32_t rb0 = lds_addr(krr) + (uint32_t)(kw * 32 * 64 + rdl.off[0]);
-        const uint32_t rb1 = lds_addr(krr) + (uint32_t)(kw * 32 * 64 + rdl.off[1]);
-        static_for<C::KSR>([&](auto s) {
+#pragma unroll
+      for (int j = 0; j < C::KPW; ++j) {
+        const uint32_t row = (uint32_t)((kw * C::KPW + j) * 32 * 64);
+        const uint32_t kb0 = lds_addr(krk) + row + (uint32_t)rdl.off[0];
+        const uint32_t kb1 = lds_addr(krk) + row + (uint32_t)rdl.off[1];
+        static_for<C::KSD>([&](auto s) {
           constexpr int S = decltype(s)::value;
-          ds_read16_inplace<(S >> 1) * C::BN * 64>(kreg[C::KSD + S], (S & 1) ? rb1 : rb0);
+          ds_read16_inplace<(S >> 1) * C::BN * 64>(kreg[j][S], (S & 1) ? kb1 : kb0);
         });
+        if constexpr (C::KSR > 0) {
+          const uint32_t rb0 = lds_addr(krr) + row + (uint32_t)rdl.off[0];
+          const uint32_t rb1 = lds_addr(krr) + row + (uint32_t)rdl.off[1];
+          static_for<C::KSR>([&](auto s) {
+            constexpr int S = decltype(s)::value;
+            ds_read16_inplace<(S >> 1) * C::BN * 64>(kreg[j][C::KSD + S], (S & 1) ? rb1 : rb0);
+          });
+        }
       }
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     };
@@ -346,9 +363,11 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     auto sign_k = [&]() {
       if (p.qa != 1.f) {
 #pragma unroll
-        for (int s = 0; s < C::KSD; ++s)
+        for (int j = 0; j < C::KPW; ++j)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) kreg[s][i] = (kreg[s][i] & kand) ^ kxor;
+          for (int s = 0; s < C::KSD; ++s)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) kreg[j][s][i] = (kreg[j][s][i] & kand) ^ kxor;
       }
     };
 
@@ -365,8 +384,8 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     // rows 8 gq + 4 hl .. +3, gq = 0..3: -LSE in lsr[gq], delta in
     // lsr[4 + gq]), read with the operands so their latency hides under the
     // MFMAs.
-    auto scores = [&](const KvCursor& c, const uint8_t* cur, f32x16& sacc, f32x16& dpacc,
-                      f32x4_t (&lsr)[8]) {
+    auto scores = [&](const KvCursor& c, const uint8_t* cur, f32x16 (&sacc)[C::KPW],
+                      f32x16 (&dpacc)[C::KPW], f32x4_t (&lsr)[8]) {
       // (A vanilla head, or rank padding, has zero rank operands: its rank
       // MFMAs add exact zeros and keep the block one basic block.)
       const uint8_t* qt = cur;
@@ -389,38 +408,58 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       }
       // S / c = b Rq Rk^T + Q (a K)^T: the rank chain, scaled by b in fp32,
       // then the head-dim chain on top, interleaved with the dP chain.
-      sacc = f32x16{};
-      dpacc = f32x16{};
+      // (Every operand read serves the wave's KPW key slices.)
 #pragma unroll
-      for (int s = 0; s < C::KSR; ++s) sacc = mfma32(qa[C::KSD + s], as_bf16x8(kreg[C::KSD + s]), sacc);
-      if constexpr (C::KSR > 0) sacc *= bhp;
-#pragma unroll
-      for (int s = 0; s < C::KSD; ++s) {
-        sacc = mfma32(qa[s], as_bf16x8(kreg[s]), sacc);
-        dpacc = mfma32(oa[s], as_bf16x8(vreg[s]), dpacc);
+      for (int j = 0; j < C::KPW; ++j) {
+        sacc[j] = f32x16{};
+        dpacc[j] = f32x16{};
       }
+#pragma unroll
+      for (int s = 0; s < C::KSR; ++s)
+#pragma unroll
+        for (int j = 0; j < C::KPW; ++j)
+          sacc[j] = mfma32(qa[C::KSD + s], as_bf16x8(kreg[j][C::KSD + s]), sacc[j]);
+      if constexpr (C::KSR > 0) {
+#pragma unroll
+        for (int j = 0; j < C::KPW; ++j) sacc[j] *= bhp;
+      }
+#pragma unroll
+      for (int s = 0; s < C::KSD; ++s)
+#pragma unroll
+        for (int j = 0; j < C::KPW; ++j) {
+          sacc[j] = mfma32(qa[s], as_bf16x8(kreg[j][s]), sacc[j]);
+          dpacc[j] = mfma32(oa[s], as_bf16x8(vreg[j][s]), dpacc[j]);
+        }
       // issue order: every read, then the rank MFMAs, then (after the
-      // scaling) the head-dim MFMAs of S and dP
-      __builtin_amdgcn_sched_group_barrier(0x100, 2 * C::KSD + C::KSR + 8, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, C::KSR, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2 * C::KSD, 0);
+      // scaling) the head-dim MFMAs of S and dP.  With two key slices the
+      // -LSE / delta reads go after the MFMAs (their latency still hides
+      // under them), so that those registers are not live with the operands.
+      constexpr int LSR_FIRST = C::KPW == 1 ? 8 : 0;
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * C::KSD + C::KSR + LSR_FIRST, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, C::KSR * C::KPW, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * C::KSD * C::KPW, 0);
+      if constexpr (LSR_FIRST == 0) __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
     };
     // P = exp(S - LSE) and dS = P (dP - delta) to LDS in the B-operand layout
     // of the consumer's MFMAs: for k-half j (query rows 16j..16j+15), lane
     // (key l32, half hl) holds rows 16j + 8i + 4hl + e, i = 0..1, e = 0..3,
     // i.e. accumulator registers 8j..8j+7.
-    auto softmax = [&](const KvCursor& c, uint8_t* pd, const f32x16& sacc,
-                       const f32x16& dpacc, const f32x4_t (&lsr)[8]) {
+    auto softmax = [&](const KvCursor& c, uint8_t* pd, const f32x16 (&sacc_)[C::KPW],
+                       const f32x16 (&dpacc_)[C::KPW], const f32x4_t (&lsr)[8]) {
       const KvItem& x = c.it;
       const int qbase = (x.qb_lo + c.qi) * C::BM;
+#pragma unroll
+      for (int ks = 0; ks < C::KPW; ++ks) {
+      const f32x16& sacc = sacc_[ks];
+      const f32x16& dpacc = dpacc_[ks];
       // Zero-filled query rows (past the sequence) have Q = dO = LSE =
       // delta = 0, so P (dP - delta) = 0 there; columns of keys past the
       // sequence are never stored.  Only the causal diagonal needs a mask:
       // query row qbase + r sees key k0t + krow iff r >= thr.  Blocks off
       // the diagonal (every block of a non-causal problem) skip the compare
       // and select, a fifth of the arithmetic per score.
-      const bool diag = p.causal && x.k0t + kw * 32 + 31 > qbase;  // wave-uniform
-      const int thr = x.k0t + krow - qbase;
+      const bool diag = p.causal && x.k0t + (kw * C::KPW + ks) * 32 + 31 > qbase;  // wave-uniform
+      const int thr = x.k0t + krow_of(ks) - qbase;
       auto body = [&](auto masked) {
         u32x4 pk[2], dk[2];
 #pragma unroll
@@ -444,7 +483,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
           dk[gq >> 1][2 * (gq & 1)] = pack_bf16(dv[0], dv[1]);
           dk[gq >> 1][2 * (gq & 1) + 1] = pack_bf16(dv[2], dv[3]);
         }
-        uint8_t* o = pd + kw * C::PW + lane * 16;
+        uint8_t* o = pd + kw * C::PW + ks * 4096 + lane * 16;
         st16(o, pk[0]);
         st16(o + 1024, pk[1]);
         st16(o + 2048, dk[0]);
@@ -454,6 +493,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
         body(std::true_type{});
       else
         body(std::false_type{});
+      }
     };
 
     // The ring: every step issues exactly C::NB VMEM instructions (the DMA
@@ -501,7 +541,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       KvCursor nx = pc;
       advance(nx, no_zero);
       const bool act = block_active(pc);
-      f32x16 sacc, dpacc;
+      f32x16 sacc[C::KPW], dpacc[C::KPW];
       f32x4_t lsr[8];
       __builtin_amdgcn_sched_barrier(0);
       if (act) scores(pc, cur, sacc, dpacc, lsr);
@@ -547,12 +587,15 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
   } else {
     // ============================ consumers ============================
     const TrLane tl(lane);
-    f32x16 dvacc[C::NDB];
-    f32x16 dkacc[C::NDB + C::NRB];
+    f32x16 dvacc[C::KPW][C::NDB];
+    f32x16 dkacc[C::KPW][C::NDB + C::NRB];
+    static_for<C::KPW>([&](auto jj) {
+      constexpr int j = decltype(jj)::value;
 #pragma unroll
-    for (int i = 0; i < C::NDB; ++i) dvacc[i] = f32x16{};
+      for (int i = 0; i < C::NDB; ++i) dvacc[j][i] = f32x16{};
 #pragma unroll
-    for (int i = 0; i < C::NDB + C::NRB; ++i) dkacc[i] = f32x16{};
+      for (int i = 0; i < C::NDB + C::NRB; ++i) dkacc[j][i] = f32x16{};
+    });
 
     // dRk of head h = graph_scale[h] acc_R (zero: an item no query block sees).
     // Lane (key l32, half hl) holds features 32 t + 8 i + 4 hl + e of its key
@@ -569,35 +612,39 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       if constexpr (C::NRB > 0) {
         if (h < p.H_G) {
           const float sr = zero ? 0.f : *const_space(params_here()->gs + h);
-          u32x4 w[C::NRB][2];
-#pragma unroll
-          for (int f = 0; f < C::NRB; ++f)
-#pragma unroll
-            for (int u = 0; u < 2; ++u) w[f][u] = swap8(dkacc[C::NDB + f], sr, zero, u);
-          const int key = x.k0t + krow;
-          if (key < x.e.lk) {
-            const TView vd = view_of(&params_here()->drk);
-            uint16_t* rp = seq_base<uint16_t>(vd, p, x.b, x.e.k0, h) + (int64_t)key * vd.ss + 8 * hl;
+          static_for<C::KPW>([&](auto jj) {
+            constexpr int j = decltype(jj)::value;
+            u32x4 w[C::NRB][2];
 #pragma unroll
             for (int f = 0; f < C::NRB; ++f)
 #pragma unroll
-              for (int u = 0; u < 2; ++u)
-                if (32 * f + 16 * u + 8 * hl < p.R) *(u32x4*)(rp + 32 * f + 16 * u) = w[f][u];
-          }
+              for (int u = 0; u < 2; ++u) w[f][u] = swap8(dkacc[j][C::NDB + f], sr, zero, u);
+            const int key = x.k0t + krow_of(j);
+            if (key < x.e.lk) {
+              const TView vd = view_of(&params_here()->drk);
+              uint16_t* rp =
+                  seq_base<uint16_t>(vd, p, x.b, x.e.k0, h) + (int64_t)key * vd.ss + 8 * hl;
+#pragma unroll
+              for (int f = 0; f < C::NRB; ++f)
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+                  if (32 * f + 16 * u + 8 * hl < p.R) *(u32x4*)(rp + 32 * f + 16 * u) = w[f][u];
+            }
+          });
         }
       }
     };
     // dK = a c acc_D and dV, 16 bytes per lane straight from the
     // accumulators: a store writes 32 contiguous bytes of each of the wave's
     // 32 rows.
-    auto write_rows = [&](const KvItem& x, const f32x16* acc, float sc, bool zero,
+    auto write_rows = [&](const KvItem& x, int j, const f32x16* acc, float sc, bool zero,
                           const TView& out) {
       u32x4 w[C::NDB][2];
 #pragma unroll
       for (int t = 0; t < C::NDB; ++t)
 #pragma unroll
         for (int u = 0; u < 2; ++u) w[t][u] = swap8(acc[t], sc, zero, u);
-      const int key = x.k0t + krow;
+      const int key = x.k0t + krow_of(j);
       if (key < x.e.lk) {
         uint16_t* rp = seq_base<uint16_t>(out, p, x.b, x.e.k0, x.kvh) + (int64_t)key * out.ss + 8 * hl;
 #pragma unroll
@@ -608,8 +655,11 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     };
     auto write_dkdv = [&](const KvItem& x, bool zero) {
       const ParamsPtr pp = params_here();
-      write_rows(x, dkacc, p.qa * p.c, zero, view_of(&pp->dk));
-      write_rows(x, dvacc, 1.f, zero, view_of(&pp->dv));
+      static_for<C::KPW>([&](auto jj) {
+        constexpr int j = decltype(jj)::value;
+        write_rows(x, j, dkacc[j], p.qa * p.c, zero, view_of(&pp->dk));
+        write_rows(x, j, dvacc[j], 1.f, zero, view_of(&pp->dv));
+      });
     };
     auto on_zero = [&](const KvItem& x) {
       write_dkdv(x, true);
@@ -648,27 +698,58 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       const uint8_t* qt = cur;
       const uint8_t* rt = cur + C::QB;
       const uint8_t* ot = cur + C::QB + C::RB;
+      // Every transposed operand read serves the wave's KPW key slices.  One
+      // slice reads its P and dS operands first; two read them one k-half
+      // at a time (registers).
+      auto mfmas = [&](int j, const bf16x8* pbj, const bf16x8* dbj) {
+#pragma unroll
+        for (int d = 0; d < C::NDB; ++d) {
+          const bf16x8 a = tr_operand<C::BM>(ot, tl, 16 * j, 32 * d);
+#pragma unroll
+          for (int ks = 0; ks < C::KPW; ++ks) dvacc[ks][d] = mfma32(a, pbj[ks], dvacc[ks][d]);
+        }
+#pragma unroll
+        for (int d = 0; d < C::NDB; ++d) {
+          const bf16x8 a = tr_operand<C::BM>(qt, tl, 16 * j, 32 * d);
+#pragma unroll
+          for (int ks = 0; ks < C::KPW; ++ks) dkacc[ks][d] = mfma32(a, dbj[ks], dkacc[ks][d]);
+        }
+#pragma unroll
+        for (int f = 0; f < C::NRB; ++f) {
+          const bf16x8 a = tr_operand<C::BM>(rt, tl, 16 * j, 32 * f);
+#pragma unroll
+          for (int ks = 0; ks < C::KPW; ++ks)
+            dkacc[ks][C::NDB + f] = mfma32(a, dbj[ks], dkacc[ks][C::NDB + f]);
+        }
+      };
       const uint8_t* o = pd + kw * C::PW + lane * 16;
-      bf16x8 pb[2], db[2];
-      pb[0] = as_bf16x8(ld16(o));
-      pb[1] = as_bf16x8(ld16(o + 1024));
-      db[0] = as_bf16x8(ld16(o + 2048));
-      db[1] = as_bf16x8(ld16(o + 3072));
+      if constexpr (C::KPW == 1) {
+        bf16x8 pb[2][1], db[2][1];
+        pb[0][0] = as_bf16x8(ld16(o));
+        pb[1][0] = as_bf16x8(ld16(o + 1024));
+        db[0][0] = as_bf16x8(ld16(o + 2048));
+        db[1][0] = as_bf16x8(ld16(o + 3072));
+        mfmas(0, pb[0], db[0]);
+        mfmas(1, pb[1], db[1]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        pipe_lds_mfma<2 * (2 * C::NDB + C::NRB), 2, 3>();
+      } else {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < 2; ++j) {
+          bf16x8 pbj[C::KPW], dbj[C::KPW];
 #pragma unroll
-        for (int d = 0; d < C::NDB; ++d)
-          dvacc[d] = mfma32(tr_operand<C::BM>(ot, tl, 16 * j, 32 * d), pb[j], dvacc[d]);
+          for (int ks = 0; ks < C::KPW; ++ks) {
+            pbj[ks] = as_bf16x8(ld16(o + ks * 4096 + j * 1024));
+            dbj[ks] = as_bf16x8(ld16(o + ks * 4096 + 2048 + j * 1024));
+          }
+          mfmas(j, pbj, dbj);
+        }
 #pragma unroll
-        for (int d = 0; d < C::NDB; ++d)
-          dkacc[d] = mfma32(tr_operand<C::BM>(qt, tl, 16 * j, 32 * d), db[j], dkacc[d]);
-#pragma unroll
-        for (int f = 0; f < C::NRB; ++f)
-          dkacc[C::NDB + f] =
-              mfma32(tr_operand<C::BM>(rt, tl, 16 * j, 32 * f), db[j], dkacc[C::NDB + f]);
+        for (int j = 0; j < 2; ++j) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 2 * C::KPW, 0);
+          pipe_lds_mfma<2 * C::NDB + C::NRB, 2, 2, C::KPW>();
+        }
       }
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-      pipe_lds_mfma<2 * (2 * C::NDB + C::NRB), 2, 3>();
     };
 
     // The last workgroup's consumers also reduce the dQ kernel's d_gs
@@ -718,14 +799,17 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       const bool last_head = cc.hi + 1 == p.group;
       write_drk(x, x.kvh * p.group + cc.hi, false);
       if (last_head) write_dkdv(x, false);
+      static_for<C::KPW>([&](auto jj) {
+        constexpr int j = decltype(jj)::value;
 #pragma unroll
-      for (int i = C::NDB; i < C::NDB + C::NRB; ++i) dkacc[i] = f32x16{};
-      if (last_head) {
+        for (int i = C::NDB; i < C::NDB + C::NRB; ++i) dkacc[j][i] = f32x16{};
+        if (last_head) {
 #pragma unroll
-        for (int i = 0; i < C::NDB; ++i) dvacc[i] = f32x16{};
+          for (int i = 0; i < C::NDB; ++i) dvacc[j][i] = f32x16{};
 #pragma unroll
-        for (int i = 0; i < C::NDB; ++i) dkacc[i] = f32x16{};
-      }
+          for (int i = 0; i < C::NDB; ++i) dkacc[j][i] = f32x16{};
+        }
+      });
       advance(cc, on_zero);
     };
     // Stage and P/dS buffer of block t - 1: st[(t + 3) % 4], pd[(t + 1) % 2].

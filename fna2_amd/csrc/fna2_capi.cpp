@@ -19,7 +19,6 @@ using fna2::kDqBN;
 using fna2::kFwdBM;
 using fna2::kFwdBN;
 using fna2::kKvBM;
-using fna2::kKvBN;
 
 constexpr size_t kAlign = 256;
 constexpr int64_t kMaxGrid = (int64_t)1 << 24;  // workgroups per launch
@@ -83,23 +82,29 @@ struct Grids {
   int64_t q_tiles = 0;    // dQ query tiles (varlen: bound)
 };
 
+// Keys per dK/dV item of the problem.
+int kv_tile(const fna2_problem& p) {
+  return fna2::kv_bn(p.head_dim, fna2::padded_rank32(p.heads_graph, p.rank));
+}
+
 Grids grids(const fna2_problem& p) {
   Grids g;
   if (p.batch <= 0) return g;
+  const int kbn = kv_tile(p);
   if (p.varlen) {
     g.fwd_bound = fna2::tile_bound(p.total_q, p.batch, kFwdBM);
     g.fwd_grid = g.fwd_bound * p.heads;
     g.dq_bound = fna2::tile_bound(p.total_q, p.batch, kDqBM);
     g.dq_grid = g.dq_bound * p.heads;
-    g.kv_bound = fna2::tile_bound(p.total_k, p.batch, kKvBN);
+    g.kv_bound = fna2::tile_bound(p.total_k, p.batch, kbn);
     g.kv_grid = g.kv_bound * p.heads_kv;
     g.kv_tiles = g.kv_bound;
     g.q_tiles = g.dq_bound;
   } else {
     g.fwd_grid = (int64_t)p.batch * cdiv64(p.seqlen_q, kFwdBM) * p.heads;
     g.dq_grid = (int64_t)p.batch * cdiv64(p.seqlen_q, kDqBM) * p.heads;
-    g.kv_grid = (int64_t)p.batch * cdiv64(p.seqlen_k, kKvBN) * p.heads_kv;
-    g.kv_tiles = (int64_t)p.batch * cdiv64(p.seqlen_k, kKvBN);
+    g.kv_grid = (int64_t)p.batch * cdiv64(p.seqlen_k, kbn) * p.heads_kv;
+    g.kv_tiles = (int64_t)p.batch * cdiv64(p.seqlen_k, kbn);
     g.q_tiles = (int64_t)p.batch * cdiv64(p.seqlen_q, kDqBM);
   }
   return g;
@@ -444,7 +449,7 @@ int fwd_launch(const fna2_fwd_args* a, void* ws, hipStream_t stream) {
     fna2::TileRec* tiles = (fna2::TileRec*)(pl + L.tiles_q);
     int* count = (int*)(pl + L.count_q);
     const fna2::TileList lq{{0, kFwdBM, kFwdBN, 1}, tiles, count, (int)g.fwd_bound};
-    const fna2::TileList lk{{1, kKvBN, kKvBM, 0}, (fna2::TileRec*)(pl + L.tiles_k),
+    const fna2::TileList lk{{1, kv_tile(p), kKvBM, 0}, (fna2::TileRec*)(pl + L.tiles_k),
                             (int*)(pl + L.count_k), (int)g.kv_bound};
     if (fna2::launch_build_tiles(K.p, lq, &lk, nullptr, stream) != hipSuccess)
       return FNA2_E_LAUNCH;
@@ -585,7 +590,7 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
       fna2::TileRec* tk = (fna2::TileRec*)((char*)a->workspace + w.tiles_k);
       int* ck = (int*)((char*)a->workspace + w.count_k);
       const fna2::TileList lq{{0, kDqBM, kDqBN, 1}, tq, cq, (int)g.dq_bound};
-      const fna2::TileList lk{{1, kKvBN, kKvBM, 0}, tk, ck, (int)g.kv_bound};
+      const fna2::TileList lk{{1, kv_tile(p), kKvBM, 0}, tk, ck, (int)g.kv_bound};
       const fna2::ZeroRows zero{K.dq, K.drq, K.dk, K.dv, K.drk,
                                 (int)std::max(p.total_q, p.total_k)};
       if (fna2::launch_build_tiles(K.p, lq, &lk, &zero, stream) != hipSuccess)

@@ -37,9 +37,15 @@ struct BwdParams {
 // varlen tile list sorts by.
 constexpr int kFwdBM = 128;
 constexpr int kFwdBN = 64;
-// Backward: dK/dV kernel tiles keys by kKvBN and walks queries kKvBM at a
-// time; the dQ kernel tiles queries by kDqBM and walks keys kDqBN at a time.
-constexpr int kKvBN = 128;
+// Backward: the dK/dV kernel tiles keys by kv_bn(D, rank tile) and walks
+// queries kKvBM at a time; the dQ kernel tiles queries by kDqBM and walks
+// keys kDqBN at a time.  A dK/dV item is four producer waves of kv_kpw
+// 32-key slices: two at d = 64 with a rank tile of at most 32 (the rows and
+// accumulators of 64 keys fit a wave's registers there, and each block's
+// operand reads, DMA and barrier then serve twice the MFMAs), one
+// otherwise.
+constexpr int kv_kpw(int D, int rpl) { return (D == 64 && rpl <= 32) ? 2 : 1; }
+constexpr int kv_bn(int D, int rpl) { return 128 * kv_kpw(D, rpl); }
 constexpr int kKvBM = 32;
 constexpr int kDqBM = 128;
 constexpr int kDqBN = 64;

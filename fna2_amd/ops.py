@@ -35,19 +35,27 @@ from .flash_naylis_attn import (_fna2_backward, _fna2_backward_varlen, _fna2_for
 # Tile shapes of the varlen lists (the forward / dQ query tiles and the
 # dK/dV key tiles, fna2_kernels.h) and the record size.
 _QUERY_TILE = 128
-_KEY_TILE = 128
 _TILE_RECORD = 32
 _ALIGN = 256
 
 
-def plan_nbytes(total_q, total_k, nseq) -> int:
-    """Bytes of a varlen plan (fna2_plan_bytes), from the token counts and
-    the number of sequences; works on symbolic sizes."""
+def key_tile(head_dim: int, heads_graph: int, rank: int) -> int:
+    """Keys per dK/dV item (kv_bn in fna2_kernels.h): 256 at d = 64 with a
+    rank tile of at most 32, else 128."""
+    rpl = (rank + 31) // 32 * 32 if heads_graph > 0 and rank > 0 else 0
+    return 256 if head_dim == 64 and rpl <= 32 else 128
+
+
+def plan_nbytes(total_q, total_k, nseq, head_dim=128, heads_graph=0, rank=0) -> int:
+    """Bytes of a varlen plan (fna2_plan_bytes), from the token counts, the
+    number of sequences and the shape that sets the key tile; works on
+    symbolic sizes."""
     if nseq <= 0:
         return 0
     up = lambda x: (x + _ALIGN - 1) // _ALIGN * _ALIGN
+    kt = key_tile(head_dim, heads_graph, rank)
     tiles_q = (total_q + _QUERY_TILE - 1) // _QUERY_TILE + nseq
-    tiles_k = (total_k + _KEY_TILE - 1) // _KEY_TILE + nseq
+    tiles_k = (total_k + kt - 1) // kt + nseq
     return up(_TILE_RECORD * tiles_q) + _ALIGN + up(_TILE_RECORD * tiles_k) + _ALIGN
 
 
@@ -94,7 +102,9 @@ def _fna2_fwd_fake(q, k, v, r_q, r_k, graph_scale, softmax_scale, is_causal, cu_
         plan = q.new_empty((0,), dtype=torch.uint8)
     else:
         lse = q.new_empty((q.shape[1], q.shape[0]), dtype=torch.float32).t()  # head-major
-        nbytes = plan_nbytes(q.shape[0], k.shape[0], cu_seqlens_q.shape[0] - 1)
+        hg = 0 if r_q is None else r_q.shape[1]
+        nbytes = plan_nbytes(q.shape[0], k.shape[0], cu_seqlens_q.shape[0] - 1, q.shape[-1], hg,
+                             0 if r_q is None else r_q.shape[-1])
         plan = q.new_empty((nbytes,), dtype=torch.uint8)
     return out, lse, plan
 

@@ -31,10 +31,12 @@ def test_plan_size_closed_form_matches_library():
         pytest.skip("libfna2_hip.so not built")
     lib = _capi.lib()
     for tq, tk, n in [(16384, 16384, 64), (1, 5, 1), (32768, 32768, 385), (0, 10, 2),
-                      (1000, 2000, 7), (5, 0, 3), (128, 128, 1), (129, 257, 2)]:
-        prob = F._problem(True, n, 0, 0, tq, tk, 16, 16, 16, 128, 32, True, 0.1)
-        prob.cu_seqlens_q = prob.cu_seqlens_k = 0x1000
-        assert lib.fna2_plan_bytes(ctypes.byref(prob)) == ops.plan_nbytes(tq, tk, n), (tq, tk, n)
+                      (1000, 2000, 7), (5, 0, 3), (128, 128, 1), (129, 257, 2), (300, 513, 2)]:
+        for D, HG, R in [(128, 16, 32), (64, 8, 16), (64, 8, 64), (64, 0, 0), (128, 4, 64)]:
+            prob = F._problem(True, n, 0, 0, tq, tk, 16, 16, HG, D, R, True, 0.1)
+            prob.cu_seqlens_q = prob.cu_seqlens_k = 0x1000
+            assert lib.fna2_plan_bytes(ctypes.byref(prob)) == ops.plan_nbytes(tq, tk, n, D, HG, R), \
+                (tq, tk, n, D, HG, R)
     assert ops.plan_nbytes(100, 100, 0) == 0
 
 
@@ -58,7 +60,7 @@ def test_fake_forward_metadata():
         out, lse, plan = torch.ops.fna2.fwd(qv, kv, vv, rqv, rkv, gs, 0.088, True, cu, cu, 300,
                                             300)
         assert out.shape == qv.shape and lse.shape == (T, Hq)
-        assert plan.dtype == torch.uint8 and plan.numel() == ops.plan_nbytes(T, T, N)
+        assert plan.dtype == torch.uint8 and plan.numel() == ops.plan_nbytes(T, T, N, D, Hq, R)
         g = torch.ops.fna2.bwd(mk(T, Hq, D), qv, kv, vv, rqv, rkv, gs, out, lse, plan, 0.088,
                                True, cu, cu, 300, 300)
         assert [tuple(t.shape) for t in g] == [tuple(qv.shape), tuple(kv.shape), tuple(vv.shape),
