@@ -4,14 +4,15 @@
 // (FNA2/flash_naylis_attn.py:390-553, :929-1076).
 //
 // Persistent: one workgroup per CU walks a list of work items, an item being
-// the 128 keys of one key tile of one KV head; workgroup g takes items
+// the keys of one key tile (4 waves x KPW slices of 32) of one KV head;
+// workgroup g takes items
 // g, 2G-1-g, 2G+g, ... (snake order over a longest-first list).  For each
 // query head of the GQA group an item walks the 32-query blocks that can see
 // its keys (causal: from the key tile's diagonal on).
 //
 // The workgroup's 8 waves split the work by role, two waves per SIMD:
-//   * producer wave w (0-3) keeps the K | Rk and V rows of keys 32w..32w+31
-//     in registers (B operands, one key per lane) and per block forms
+//   * producer wave w (0-3) keeps the K | Rk and V rows of its KPW slices of
+//     32 keys in registers (B operands, one key per lane) and per block forms
 //       S, dP  (32 x 32)               A operands: Q | Rq and dO rows
 //       P = exp(S - LSE),  dS = P (dP - delta)
 //     and stores P and dS, already in MFMA operand layout, to LDS;
@@ -213,7 +214,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     if (++c.hi >= p.group) next_item(c, no_zero);
     return c;
   };
-  // Whether this wave's 32 keys meet block qi of the cursor's item.
+  // Whether this wave's keys meet block qi of the cursor's item.
   auto block_active = [&](const KvCursor& c) {
     const int wk0 = c.it.k0t + kw * 32 * C::KPW;
     const int qbase = (c.it.qb_lo + c.qi) * C::BM;
@@ -379,7 +380,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       return uni_f(h < p.H_G ? *const_space(params_here()->gs + h) / p.c : 0.f);
     };
 
-    // S and dP of this wave's 32 keys against block qi of the cursor.
+    // S and dP of this wave's key slices against block qi of the cursor.
     // The block's -LSE log2(e) and delta rows go to lsr (this lane's query
     // rows 8 gq + 4 hl .. +3, gq = 0..3: -LSE in lsr[gq], delta in
     // lsr[4 + gq]), read with the operands so their latency hides under the
