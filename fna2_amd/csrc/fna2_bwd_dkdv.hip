@@ -654,13 +654,23 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
           for (int u = 0; u < 2; ++u) *(u32x4*)(rp + 32 * t + 16 * u) = w[t][u];
       }
     };
-    auto write_dkdv = [&](const KvItem& x, bool zero) {
+    auto write_dk = [&](const KvItem& x, bool zero) {
       const ParamsPtr pp = params_here();
       static_for<C::KPW>([&](auto jj) {
         constexpr int j = decltype(jj)::value;
         write_rows(x, j, dkacc[j], p.qa * p.c, zero, view_of(&pp->dk));
+      });
+    };
+    auto write_dv = [&](const KvItem& x, bool zero) {
+      const ParamsPtr pp = params_here();
+      static_for<C::KPW>([&](auto jj) {
+        constexpr int j = decltype(jj)::value;
         write_rows(x, j, dvacc[j], 1.f, zero, view_of(&pp->dv));
       });
+    };
+    auto write_dkdv = [&](const KvItem& x, bool zero) {
+      write_dk(x, zero);
+      write_dv(x, zero);
     };
     auto on_zero = [&](const KvItem& x) {
       write_dkdv(x, true);
@@ -762,7 +772,25 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     start(cc, on_zero);
     // Step t consumes block t - 1 (nothing at t = 0).  The barrier does not
     // wait for the consumers' own stores.
+    //
+    // An item's dV is stored at the start of the next step, not with its
+    // dK: the step that ends an item is the consumers' longest (its stores)
+    // while the producers start the next item, and the one after it is the
+    // producers' longest while the consumers have one block to consume.
     bool first = true;
+    bool dv_pending = false;
+    KvItem dv_item{};
+    auto flush_dv = [&]() {
+      if (dv_pending) {
+        write_dv(dv_item, false);
+        static_for<C::KPW>([&](auto jj) {
+          constexpr int j = decltype(jj)::value;
+#pragma unroll
+          for (int i = 0; i < C::NDB; ++i) dvacc[j][i] = f32x16{};
+        });
+        dv_pending = false;
+      }
+    };
     auto step = [&](const uint8_t* cur, uint8_t* pd) {
       if constexpr (C::KR) {
         // The producers switch to the next (item, head) at this step and
@@ -778,6 +806,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
         first = false;
         return;
       }
+      flush_dv();
       if (cc.done) return;
       if (block_active(cc)) consume(cur, pd);
       if constexpr (C::KR) {
@@ -799,14 +828,16 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       const KvItem x = cc.it;
       const bool last_head = cc.hi + 1 == p.group;
       write_drk(x, x.kvh * p.group + cc.hi, false);
-      if (last_head) write_dkdv(x, false);
+      if (last_head) {
+        write_dk(x, false);
+        dv_pending = true;
+        dv_item = x;
+      }
       static_for<C::KPW>([&](auto jj) {
         constexpr int j = decltype(jj)::value;
 #pragma unroll
         for (int i = C::NDB; i < C::NDB + C::NRB; ++i) dkacc[j][i] = f32x16{};
         if (last_head) {
-#pragma unroll
-          for (int i = 0; i < C::NDB; ++i) dvacc[j][i] = f32x16{};
 #pragma unroll
           for (int i = 0; i < C::NDB; ++i) dkacc[j][i] = f32x16{};
         }
@@ -824,6 +855,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       step(st2, pd0);
       if (cc.done) break;
     }
+    flush_dv();  // the last item's dV
   }
 }
 
