@@ -50,6 +50,8 @@ namespace fna2 {
 
 namespace {
 
+enum : unsigned { kTileQ = 1, kTileR = 2, kTileO = 4, kTileL = 8, kTileAll = 15 };
+
 template <int D, int RPL>
 struct KvCfg {
   static constexpr int NP = 4;       // producer waves (as many consumers)
@@ -81,9 +83,21 @@ struct KvCfg {
   static constexpr bool KR = 4 * STAGE + 2 * PDS + KRK + KRR <= 160 * 1024;
   using DmaKK = Dma<BN, CD, NP>;
   using DmaKR = Dma<BN, CR, NP>;
-  // VMEM instructions every producer wave issues per block (Q, dO, rank
-  // operand, one -LSE log2(e) / delta row), the same for every wave.
-  static constexpr int NB = 2 * DmaD::PER_WAVE + (RPL > 0 ? DmaR::PER_WAVE : 0) + 1;
+  // The ring tiles of a block: Q, the rank operand, dO and the -LSE log2(e)
+  // / delta rows.  CDMA: those the consumer waves DMA (at the start of their
+  // step); the producers DMA the rest (at the end of theirs).  With two key
+  // slices per wave the consumers have the time for all of them; with one
+  // their own step is the longer with any (measured), and the producers
+  // keep them.
+  static constexpr unsigned CDMA = KPW == 2 ? kTileAll : 0u;
+  // VMEM instructions per wave and block for the tiles in mask m.
+  static constexpr int nb_of(unsigned m) {
+    return ((m & kTileQ) ? DmaD::PER_WAVE : 0) +
+           ((m & kTileR) && RPL > 0 ? DmaR::PER_WAVE : 0) +
+           ((m & kTileO) ? DmaD::PER_WAVE : 0) + ((m & kTileL) ? 1 : 0);
+  }
+  static constexpr int NBC = nb_of(CDMA);              // per consumer wave
+  static constexpr int NBP = nb_of(kTileAll & ~CDMA);  // per producer wave
 };
 
 // Scheduling pattern for a region of n operands, each `per` LDS reads that
@@ -133,6 +147,74 @@ struct KvCursor {
   int r, hi, qi;
   bool done;
   KvItem it;
+};
+
+// One role's share of the ring DMA: the tiles in MASK of a block, wave w of
+// the role issuing exactly C::nb_of(MASK) VMEM instructions per block.
+// Waves 0 and 2 of the role fetch the -LSE log2(e) row, 1 and 3 the delta
+// row (the same bytes twice: every wave issues as many instructions).
+template <class C, int RPL, unsigned MASK>
+struct RingDma {
+  typename C::DmaD dmq, dmo;
+  typename C::DmaR dmr;
+  uint32_t qrb, orb, srb, lrb, drb, loff;
+  bool is_delta;
+  // Buffer descriptors for the issue cursor's (item, head), set when it
+  // enters one: they span the sequence's whole query range, so rows past it
+  // read as zeros, and a block only adds its row offset to the lane
+  // offsets.  (The host keeps a sequence's rows under 2 GB.)
+  u32x4 sq, so, sr, sl;
+
+  __device__ __forceinline__ void init(const BwdParams& P, int w, int lane) {
+    qrb = (uint32_t)P.q.ss * 2u;
+    orb = (uint32_t)P.dout.ss * 2u;
+    srb = (uint32_t)P.rqs.ss * 2u;
+    if constexpr ((MASK & kTileQ) != 0) dmq.init_fixed(w, lane, qrb, C::CD);
+    if constexpr ((MASK & kTileO) != 0) dmo.init_fixed(w, lane, orb, C::CD);
+    if constexpr ((MASK & kTileR) != 0 && RPL > 0) dmr.init_fixed(w, lane, srb, C::CR);
+    is_delta = (w & 1) != 0;
+    lrb = (uint32_t)P.nlse.ss * 4u;
+    drb = (uint32_t)P.delta.ss * 4u;
+    loff = (uint32_t)lane * (is_delta ? drb : lrb);
+  }
+  __device__ __forceinline__ void setup(const BwdParams& P, const KvCursor& c) {
+    const Problem& p = P.p;
+    if (c.done) {  // past the last block: the ring's last DMAs read nothing
+      sq = rsrc_words(P.q.ptr, 0u);
+      so = sq;
+      sr = sq;
+      sl = sq;
+      return;
+    }
+    const KvItem& x = c.it;
+    const int h = x.kvh * p.group + c.hi;
+    const uint32_t lq = (uint32_t)x.e.lq;
+    const ParamsPtr pp = params_here();
+    const uint16_t* qb = seq_base<const uint16_t>(view_of(&pp->q), p, x.b, x.e.q0, h);
+    if constexpr ((MASK & kTileQ) != 0) sq = rsrc_words(qb, lq * qrb);
+    if constexpr ((MASK & kTileO) != 0)
+      so = rsrc_words(seq_base<const uint16_t>(view_of(&pp->dout), p, x.b, x.e.q0, h), lq * orb);
+    if constexpr ((MASK & kTileR) != 0 && RPL > 0) {
+      const bool graph = h < p.H_G;
+      sr = rsrc_words(graph ? seq_base<const uint16_t>(view_of(&pp->rqs), p, x.b, x.e.q0, h) : qb,
+                      graph ? lq * srb : 0u);
+    }
+    if constexpr ((MASK & kTileL) != 0) {
+      const float* lb = seq_base<const float>(is_delta ? view_of(&pp->delta) : view_of(&pp->nlse),
+                                              p, x.b, x.e.q0, h);
+      sl = rsrc_words(lb, lq * (is_delta ? drb : lrb));
+    }
+  }
+  // Exactly C::nb_of(MASK) VMEM instructions, unconditionally.
+  __device__ __forceinline__ void issue(const KvCursor& c, uint8_t* st, int w) const {
+    const uint32_t q0 = c.done ? 0u : (uint32_t)((c.it.qb_lo + c.qi) * C::BM);
+    if constexpr ((MASK & kTileQ) != 0) dmq.issue_fixed(sq, st, w, q0 * qrb);
+    if constexpr ((MASK & kTileR) != 0 && RPL > 0) dmr.issue_fixed(sr, st + C::QB, w, q0 * srb);
+    if constexpr ((MASK & kTileO) != 0) dmo.issue_fixed(so, st + C::QB + C::RB, w, q0 * orb);
+    if constexpr ((MASK & kTileL) != 0)
+      dma_lds<4>(sl, lds_addr(st + C::QB + C::RB + C::OB + (is_delta ? 256 : 0)),
+                 loff + q0 * (is_delta ? drb : lrb));
+  }
 };
 
 template <int D, int RPL>
@@ -224,57 +306,6 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
   if (wv < C::NP) {
     // ============================ producers ============================
     const RowLane rdl(lane);
-    const uint32_t qrb = (uint32_t)P.q.ss * 2u, orb = (uint32_t)P.dout.ss * 2u;
-    const uint32_t srb = (uint32_t)P.rqs.ss * 2u;
-    typename C::DmaD dmq, dmo;
-    typename C::DmaR dmr;
-    dmq.init_fixed(wv, lane, qrb, C::CD);
-    dmo.init_fixed(wv, lane, orb, C::CD);
-    if constexpr (RPL > 0) dmr.init_fixed(wv, lane, srb, C::CR);
-    // Waves 0 and 2 fetch the -LSE log2(e) row of a block, 1 and 3 the delta
-    // row (the same bytes twice: every wave issues as many instructions).
-    const bool is_delta = (wv & 1) != 0;
-    const uint32_t lrb = (uint32_t)P.nlse.ss * 4u, drb = (uint32_t)P.delta.ss * 4u;
-    const uint32_t loff = (uint32_t)lane * (is_delta ? drb : lrb);
-
-    // Buffer descriptors for the issue cursor's (item, head), set when it
-    // enters one: they span the sequence's whole query range, so rows past
-    // it read as zeros, and a block only adds its row offset to the lane
-    // offsets.  (The host keeps a sequence's rows under 2 GB.)
-    u32x4 sq, so, sr, sl;
-    auto setup = [&](const KvCursor& c) {
-      if (c.done) {  // past the last block: the ring's last DMAs read nothing
-        sq = rsrc_words(P.q.ptr, 0u);
-        so = sq;
-        sr = sq;
-        sl = sq;
-        return;
-      }
-      const KvItem& x = c.it;
-      const int h = x.kvh * p.group + c.hi;
-      const uint32_t lq = (uint32_t)x.e.lq;
-      const ParamsPtr pp = params_here();
-      const uint16_t* qb = seq_base<const uint16_t>(view_of(&pp->q), p, x.b, x.e.q0, h);
-      sq = rsrc_words(qb, lq * qrb);
-      so = rsrc_words(seq_base<const uint16_t>(view_of(&pp->dout), p, x.b, x.e.q0, h), lq * orb);
-      if constexpr (RPL > 0) {
-        const bool graph = h < p.H_G;
-        sr = rsrc_words(graph ? seq_base<const uint16_t>(view_of(&pp->rqs), p, x.b, x.e.q0, h) : qb,
-                        graph ? lq * srb : 0u);
-      }
-      const float* lb = seq_base<const float>(is_delta ? view_of(&pp->delta) : view_of(&pp->nlse),
-                                              p, x.b, x.e.q0, h);
-      sl = rsrc_words(lb, lq * (is_delta ? drb : lrb));
-    };
-    // Exactly C::NB VMEM instructions, unconditionally.
-    auto issue = [&](const KvCursor& c, uint8_t* st) {
-      const uint32_t q0 = c.done ? 0u : (uint32_t)((c.it.qb_lo + c.qi) * C::BM);
-      dmq.issue_fixed(sq, st, wv, q0 * qrb);
-      if constexpr (RPL > 0) dmr.issue_fixed(sr, st + C::QB, wv, q0 * srb);
-      dmo.issue_fixed(so, st + C::QB + C::RB, wv, q0 * orb);
-      dma_lds<4>(sl, lds_addr(st + C::QB + C::RB + C::OB + (is_delta ? 256 : 0)),
-                 loff + q0 * (is_delta ? drb : lrb));
-    };
     // Stationary rows (B operands): lane holds key krow, features
     // 16s + 8hl .. +7 of k-step s: K | Rk and V of the producer's (item,
     // head), loaded in place (load16_inplace) and waited for by the ring
@@ -497,39 +528,43 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       }
     };
 
-    // The ring: every step issues exactly C::NB VMEM instructions (the DMA
-    // of block T + 2), so "wait until C::NB are in flight" at step T's
-    // barrier waits for block T's tiles and everything issued before them,
-    // and nothing newer.  The rows of the next (item, head) are loaded by
-    // the last block of the current one, after its MFMAs and before its DMA,
-    // so the next step's barrier also waits for them.  The DMA and the row
-    // loads are inline assembly, so the compiler adds no wait of its own.
+    // The producers' share of the ring: every step issues exactly C::NBP
+    // VMEM instructions (their tiles of block T + 2), so "wait until C::NBP
+    // are in flight" at step T's barrier waits for their tiles of block T
+    // and everything issued before them, and nothing newer.  The rows of the
+    // next (item, head) are loaded by the last block of the current one,
+    // after its MFMAs and before its DMA, so the next step's barrier also
+    // waits for them.  The DMA and the row loads are inline assembly, so the
+    // compiler adds no wait of its own.
+    RingDma<C, RPL, kTileAll & ~C::CDMA> ring;
+    ring.init(P, wv, lane);
     KvCursor pc;  // the block being produced
     start(pc, no_zero);
     KvCursor ic = pc;  // the block whose tiles are issued next (two ahead)
-    setup(ic);
-    if (!pc.done) {
+    auto issue = [&](uint8_t* st) {
+      if constexpr (C::NBP > 0) {
+        ring.issue(ic, st, wv);
+        if (!ic.done) {
+          advance(ic, no_zero);
+          if (ic.done || ic.qi == 0) ring.setup(P, ic);
+        }
+      }
+    };
+    if constexpr (C::NBP > 0) ring.setup(P, ic);
+    if (!uni((int)pc.done)) {  // (uniform: no masked path around the loads)
       load_k(pc.it, pc.it.kvh * p.group + pc.hi, false);
       load_v(pc.it);
     }
-    issue(ic, st0);
-    if (!ic.done) {
-      advance(ic, no_zero);
-      if (ic.done || ic.qi == 0) setup(ic);
-    }
-    issue(ic, st1);
-    if (!ic.done) {
-      advance(ic, no_zero);
-      if (ic.done || ic.qi == 0) setup(ic);
-    }
+    issue(st0);
+    issue(st1);
 
     // Block T (stage `cur`): wait for its tiles; S, dP; at the last block of
     // an (item, head), load the next one's rows into the registers just
-    // read; P, dS; start the DMA of block T + 2.  (P and dS go before the
-    // DMA: the DMA's issue can stall on the memory pipeline, and the
-    // consumers wait for P and dS.)
+    // read; P, dS; start the producers' DMA of block T + 2.  (P and dS go
+    // before the DMA: the DMA's issue can stall on the memory pipeline, and
+    // the consumers wait for P and dS.)
     auto step = [&](const uint8_t* cur, uint8_t* nxt, uint8_t* pd) {
-      ring_barrier<C::NB>();
+      ring_barrier<C::NBP>();
       if (pc.done) return;
       if (pc.qi == 0) {  // rows loaded by the previous block (or above)
         if constexpr (C::KR) {
@@ -561,11 +596,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       __builtin_amdgcn_sched_barrier(0);
       if (act) softmax(pc, pd, sacc, dpacc, lsr);
       __builtin_amdgcn_sched_barrier(0);
-      issue(ic, nxt);
-      if (!ic.done) {
-        advance(ic, no_zero);
-        if (ic.done || ic.qi == 0) setup(ic);
-      }
+      issue(nxt);
       __builtin_amdgcn_sched_barrier(0);
       pc = nx;
     };
@@ -702,6 +733,27 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
         dkr.issue_fixed(rsrc_words(rb, graph ? krows * krb2 : 0u), krr, kw, 0u);
       }
     };
+
+    // The consumers' share of the ring (C::NBC VMEM instructions per wave
+    // and step): their tiles of block T + 2, DMA'd right after step T's
+    // barrier, after the step's K | Rk DMA and before its stores.  Loads
+    // complete in issue order, so "wait until C::NBC are in flight" before
+    // the next barrier waits for their tiles of block T + 1 and every older
+    // load (the K | Rk tiles included), whatever the stores.  Without a
+    // share, the wave waits for its K | Rk DMA before the barrier at which
+    // the producers switch to it.
+    RingDma<C, RPL, C::CDMA> ring;
+    ring.init(P, kw, lane);
+    KvCursor ic;  // the block whose tiles are issued next
+    auto issue = [&](uint8_t* st) {
+      if constexpr (C::NBC > 0) {
+        ring.issue(ic, st, kw);
+        if (!ic.done) {
+          advance(ic, no_zero);
+          if (ic.done || ic.qi == 0) ring.setup(P, ic);
+        }
+      }
+    };
     bool kr_issued = false;
 
     // (acc_R of a vanilla head is built from zero tiles and never stored.)
@@ -763,6 +815,12 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       }
     };
 
+    // Tiles of blocks 0 and 1.
+    start(ic, no_zero);
+    if constexpr (C::NBC > 0) ring.setup(P, ic);
+    issue(st0);
+    issue(st1);
+
     // The last workgroup's consumers also reduce the dQ kernel's d_gs
     // partials (complete: that kernel ran before this one), before their
     // first block.
@@ -791,8 +849,8 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
         dv_pending = false;
       }
     };
-    auto step = [&](const uint8_t* cur, uint8_t* pd) {
-      if constexpr (C::KR) {
+    auto step = [&](const uint8_t* cur, uint8_t* pd, uint8_t* nxt) {
+      if constexpr (C::KR && C::NBC == 0) {
         // The producers switch to the next (item, head) at this step and
         // read its K | Rk from LDS after the barrier: this wave's DMA of it
         // must be complete.
@@ -801,18 +859,12 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
           kr_issued = false;
         }
       }
-      ring_barrier<63>();
-      if (first) {
-        first = false;
-        return;
-      }
-      flush_dv();
-      if (cc.done) return;
-      if (block_active(cc)) consume(cur, pd);
+      ring_barrier<(C::NBC > 0 ? C::NBC : 63)>();
       if constexpr (C::KR) {
-        // After the first block of an (item, head) of two or more blocks
-        // (the producers read its K | Rk before this step's barrier).
-        if (cc.qi == 0 && cc.it.nqb >= 2) {
+        // At the first block of an (item, head) of two or more blocks (the
+        // producers read its K | Rk before this step's barrier); the
+        // producers read the next one after the next barrier at the earliest.
+        if (!first && !cc.done && cc.qi == 0 && cc.it.nqb >= 2) {
           const KvCursor ny = next_seg(cc);
           if (!ny.done) {
             issue_kr(ny.it, ny.it.kvh * p.group + ny.hi);
@@ -820,6 +872,14 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
           }
         }
       }
+      issue(nxt);
+      if (first) {
+        first = false;
+        return;
+      }
+      flush_dv();
+      if (cc.done) return;
+      if (block_active(cc)) consume(cur, pd);
       if (cc.qi + 1 < cc.it.nqb) {
         ++cc.qi;
         return;
@@ -844,18 +904,21 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       });
       advance(cc, on_zero);
     };
-    // Stage and P/dS buffer of block t - 1: st[(t + 3) % 4], pd[(t + 1) % 2].
+    // Stage and P/dS buffer of block t - 1: st[(t + 3) % 4], pd[(t + 1) % 2];
+    // the DMA of block t + 2 goes to st[(t + 2) % 4], which the consumers
+    // read last at step t - 1 and the producers at step t - 2.
     for (;;) {
-      step(st3, pd1);
+      step(st3, pd1, st2);
       if (cc.done) break;
-      step(st0, pd0);
+      step(st0, pd0, st3);
       if (cc.done) break;
-      step(st1, pd1);
+      step(st1, pd1, st0);
       if (cc.done) break;
-      step(st2, pd0);
+      step(st2, pd0, st1);
       if (cc.done) break;
     }
     flush_dv();  // the last item's dV
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): no DMA in flight at exit
   }
 }
 
