@@ -33,10 +33,12 @@
 // chain scaled by b = graph_scale[h] / c in fp32, then the head-dim chain),
 // so the recomputed S equals the forward's bit for bit.
 //
-// Q, Rq, dO, -LSE log2(e) and delta tiles stream in by DMA (issued by
-// the producers) through a four-stage ring that runs two blocks ahead of the
-// producers, across item boundaries; the consumers read a stage one block
-// later.  The last block of an (item, head) loads the rows of the next one
+// Q, Rq, dO, -LSE log2(e) and delta tiles stream in by DMA through a
+// four-stage ring that runs two blocks ahead of the producers, across item
+// boundaries; the consumers read a stage one block later.  With two key
+// slices per wave the consumers issue that DMA (right after their barrier:
+// they idle while the producers compute), otherwise the producers do (the
+// consumers' own step would then be the longer).  The last block of an (item, head) loads the rows of the next one
 // into the registers its MFMAs have just read: V from memory, K | Rk from
 // LDS tiles that the consumers DMA'd during the current one (where the LDS
 // has room for them).  Both roles meet at one

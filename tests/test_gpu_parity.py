@@ -111,6 +111,14 @@ def test_varlen_mixed(gpu, causal):
     _varlen_case(gpu, lengths, 4, 64, 4, 4, 16, causal, seed=12)
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_varlen_gqa_d64(gpu, causal):
+    """d 64, rank 16 (two key slices per dK/dV wave, ring DMA by the
+    consumer waves): GQA groups of 3 with graph and vanilla heads in one
+    group, items of one block and of many, sequences of one token."""
+    _varlen_case(gpu, [3, 70, 256, 257, 31, 520, 1, 96], 6, 64, 2, 4, 16, causal, seed=31)
+
+
 def test_varlen_d64_rank_rows_past_20k(gpu):
     """d 64, 8 graph heads of rank 32: a tile's rank rows past 20 KB.  Caught a
     missing wait state between a scalar descriptor write and the inline-asm
