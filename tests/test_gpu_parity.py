@@ -119,6 +119,26 @@ def test_varlen_gqa_d64(gpu, causal):
     _varlen_case(gpu, [3, 70, 256, 257, 31, 520, 1, 96], 6, 64, 2, 4, 16, causal, seed=31)
 
 
+@pytest.mark.parametrize("seed", [112, 122, 126, 135])
+def test_varlen_random_shapes_d64(gpu, seed):
+    """Seeded random packs at d 64, rank <= 32: lengths from 0 to 600 with
+    tile multiples (32, 128, 256) and their neighbours over-represented,
+    GQA groups of 1 to 4 with any number of graph heads, causal or not."""
+    rng = np.random.default_rng(seed)
+    edges = [0, 1, 31, 32, 33, 127, 128, 129, 255, 256, 257]
+    n = int(rng.integers(3, 10))
+    lengths = [int(rng.choice(edges)) if rng.random() < 0.5 else int(rng.integers(0, 601))
+               for _ in range(n)]
+    if sum(lengths) == 0:
+        lengths[0] = 40
+    H_KV = int(rng.integers(1, 3))
+    Hq = H_KV * int(rng.integers(1, 5))
+    H_G = int(rng.integers(0, Hq + 1))
+    R = int(rng.choice([8, 16, 32])) if H_G else 0
+    causal = bool(rng.integers(0, 2))
+    _varlen_case(gpu, lengths, Hq, 64, H_KV, H_G, R, causal, seed=seed)
+
+
 def test_varlen_d64_rank_rows_past_20k(gpu):
     """d 64, 8 graph heads of rank 32: a tile's rank rows past 20 KB.  Caught a
     missing wait state between a scalar descriptor write and the inline-asm
