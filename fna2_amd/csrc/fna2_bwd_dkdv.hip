@@ -38,13 +38,13 @@
 // boundaries; the consumers read a stage one block later.  With two key
 // slices per wave the consumers issue that DMA (right after their barrier:
 // they idle while the producers compute), otherwise the producers do (the
-// consumers' own step would then be the longer).  The last block of an (item, head) loads the rows of the next one
-// into the registers its MFMAs have just read: V from memory, K | Rk from
-// LDS tiles that the consumers DMA'd during the current one (where the LDS
-// has room for them).  Both roles meet at one
-// barrier per block.  The stages are separate LDS objects and the loops are
-// unrolled by four so that the compiler can prove that reads and in-flight
-// DMA never alias.
+// consumers' own step would then be the longer).  The last block of an
+// (item, head) loads the rows of the next one into the registers its MFMAs
+// have just read: V from memory, K | Rk from LDS tiles that the consumers
+// DMA'd during the current one (where the LDS has room for them).  Both
+// roles meet at one barrier per block.  The stages are separate LDS objects
+// and the loops are unrolled by four so that the compiler can prove that
+// reads and in-flight DMA never alias.
 #include "fna2_kernels.h"
 #include "fna2_tile.h"
 
@@ -180,30 +180,26 @@ struct RingDma {
     loff = (uint32_t)lane * (is_delta ? drb : lrb);
   }
   __device__ __forceinline__ void setup(const BwdParams& P, const KvCursor& c) {
+    // Past the last block the ring's last DMAs read nothing (zero-size
+    // descriptors); no branch, so that every descriptor stays in registers.
     const Problem& p = P.p;
-    if (c.done) {  // past the last block: the ring's last DMAs read nothing
-      sq = rsrc_words(P.q.ptr, 0u);
-      so = sq;
-      sr = sq;
-      sl = sq;
-      return;
-    }
-    const KvItem& x = c.it;
-    const int h = x.kvh * p.group + c.hi;
-    const uint32_t lq = (uint32_t)x.e.lq;
+    const bool done = uni((int)c.done) != 0;
+    const int b = done ? 0 : c.it.b, q0 = done ? 0 : c.it.e.q0;
+    const int h = done ? 0 : c.it.kvh * p.group + c.hi;
+    const uint32_t lq = done ? 0u : (uint32_t)c.it.e.lq;
     const ParamsPtr pp = params_here();
-    const uint16_t* qb = seq_base<const uint16_t>(view_of(&pp->q), p, x.b, x.e.q0, h);
+    const uint16_t* qb = seq_base<const uint16_t>(view_of(&pp->q), p, b, q0, h);
     if constexpr ((MASK & kTileQ) != 0) sq = rsrc_words(qb, lq * qrb);
     if constexpr ((MASK & kTileO) != 0)
-      so = rsrc_words(seq_base<const uint16_t>(view_of(&pp->dout), p, x.b, x.e.q0, h), lq * orb);
+      so = rsrc_words(seq_base<const uint16_t>(view_of(&pp->dout), p, b, q0, h), lq * orb);
     if constexpr ((MASK & kTileR) != 0 && RPL > 0) {
       const bool graph = h < p.H_G;
-      sr = rsrc_words(graph ? seq_base<const uint16_t>(view_of(&pp->rqs), p, x.b, x.e.q0, h) : qb,
+      sr = rsrc_words(graph ? seq_base<const uint16_t>(view_of(&pp->rqs), p, b, q0, h) : qb,
                       graph ? lq * srb : 0u);
     }
     if constexpr ((MASK & kTileL) != 0) {
       const float* lb = seq_base<const float>(is_delta ? view_of(&pp->delta) : view_of(&pp->nlse),
-                                              p, x.b, x.e.q0, h);
+                                              p, b, q0, h);
       sl = rsrc_words(lb, lq * (is_delta ? drb : lrb));
     }
   }
