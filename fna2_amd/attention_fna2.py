@@ -251,41 +251,59 @@ class _StackedProjection(torch.autograd.Function):
     row block of one dW buffer (the parameters' gradients are views of it),
     and dx is one GEMM when the dY_i are consecutive column blocks of one
     buffer, else the per-block GEMMs accumulated in place: no concatenation
-    of the weights or of the gradients, and no separate additions."""
+    of the weights or of the gradients, and no separate additions.
+
+    Under autocast the GEMMs run in the forward's compute dtype (the dtype
+    of its output), as ``F.linear`` does: the backward casts x, the weights
+    and the incoming gradients to it, and returns dx in x's dtype and each
+    dW in the weights' dtype.  As for ``nn.Linear``, a weight that needs no
+    gradient gets no dW GEMM, and a block whose output did not reach the
+    loss gets ``None``."""
 
     @staticmethod
     def forward(ctx, x, w_all, sizes, *ws):
+        y = F.linear(x, w_all)
+        ctx.set_materialize_grads(False)  # an unused output's cotangent stays None
         ctx.save_for_backward(x)
         ctx.w_all = w_all
         ctx.sizes = sizes
-        return tuple(torch.split(F.linear(x, w_all), sizes, dim=-1))
+        ctx.cdtype = y.dtype
+        return tuple(torch.split(y, sizes, dim=-1))
 
     @staticmethod
     def backward(ctx, *gys):
         (x,) = ctx.saved_tensors
-        w_all, sizes = ctx.w_all, ctx.sizes
+        w_all, sizes, cd = ctx.w_all, ctx.sizes, ctx.cdtype
         E = x.shape[-1]
-        x2 = x.reshape(-1, E)
-        dw_all = torch.empty_like(w_all)
+        x2 = x.reshape(-1, E).to(cd)
+        w_c = w_all.to(cd)
+        gys = tuple(None if g is None else g.to(cd) for g in gys)
+        need_w = ctx.needs_input_grad[3:]
+        dw_all = None
+        if any(n and g is not None for n, g in zip(need_w, gys)):
+            dw_all = torch.empty_like(w_all)
         dws, r0 = [], 0
-        for g, n in zip(gys, sizes):
-            blk = dw_all[r0:r0 + n]
-            if g is None:
-                blk.zero_()
+        for g, n, need in zip(gys, sizes, need_w):
+            if g is None or not need:
+                dws.append(None)
             else:
-                torch.mm(g.reshape(-1, n).t(), x2, out=blk)
-            dws.append(blk)
+                blk = dw_all[r0:r0 + n]
+                if blk.dtype == cd:
+                    torch.mm(g.reshape(-1, n).t(), x2, out=blk)
+                else:
+                    blk.copy_(torch.mm(g.reshape(-1, n).t(), x2))
+                dws.append(blk)
             r0 += n
         dx = None
         if ctx.needs_input_grad[0]:
             stacked = _column_blocks(gys, sizes)
             if stacked is not None:
-                dx = torch.mm(stacked, w_all)
+                dx = torch.mm(stacked, w_c)
             else:
                 r0 = 0
                 for g, n in zip(gys, sizes):
                     if g is not None:
-                        g2, w = g.reshape(-1, n), w_all[r0:r0 + n]
+                        g2, w = g.reshape(-1, n), w_c[r0:r0 + n]
                         if dx is None:
                             dx = torch.mm(g2, w)
                         else:
@@ -293,7 +311,7 @@ class _StackedProjection(torch.autograd.Function):
                     r0 += n
                 if dx is None:
                     dx = torch.zeros_like(x2)
-            dx = dx.view(x.shape)
+            dx = dx.view(x.shape).to(x.dtype)
         return (dx, None, None, *dws)
 
 

@@ -54,7 +54,7 @@ namespace {
 
 enum : unsigned { kTileQ = 1, kTileR = 2, kTileO = 4, kTileL = 8, kTileAll = 15 };
 
-template <int D, int RPL>
+template <int D, int RPL, bool F16>
 struct KvCfg {
   static constexpr int NP = 4;       // producer waves (as many consumers)
   static constexpr int NW = 2 * NP;  // waves per workgroup
@@ -73,7 +73,12 @@ struct KvCfg {
   static constexpr int OB = BM * D * 2;
   static constexpr int LB = 2 * 256;  // -LSE log2(e), delta: one 64-lane dword DMA each
   static constexpr int STAGE = QB + RB + OB + LB;
-  static constexpr int PW = KPW * 4 * 1024;  // a producer's P and dS operands of one block
+  // A producer's P and dS operands of one block: per key slice, P and dS in
+  // the element type (two 16-query k-halves each), and with fp16 elements
+  // and a rank tile also dS in bf16 for the dRk chain (Rq is bf16).
+  static constexpr bool DBR = F16 && RPL > 0;
+  static constexpr int SL = (DBR ? 6 : 4) * 1024;  // bytes per key slice
+  static constexpr int PW = KPW * SL;
   static constexpr int PDS = NP * PW;
   using DmaD = Dma<BM, CD, NP>;
   using DmaR = Dma<BM, CR, NP>;
@@ -215,9 +220,9 @@ struct RingDma {
   }
 };
 
-template <int D, int RPL>
+template <int D, int RPL, bool F16>
 __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
-  using C = KvCfg<D, RPL>;
+  using C = KvCfg<D, RPL, F16>;
   __shared__ __attribute__((aligned(1024))) uint8_t st0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t st1[C::STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t st2[C::STAGE];
@@ -457,8 +462,8 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       for (int s = 0; s < C::KSD; ++s)
 #pragma unroll
         for (int j = 0; j < C::KPW; ++j) {
-          sacc[j] = mfma32(qa[s], as_bf16x8(kreg[j][s]), sacc[j]);
-          dpacc[j] = mfma32(oa[s], as_bf16x8(vreg[j][s]), dpacc[j]);
+          sacc[j] = mfma_e<F16>(qa[s], as_bf16x8(kreg[j][s]), sacc[j]);
+          dpacc[j] = mfma_e<F16>(oa[s], as_bf16x8(vreg[j][s]), dpacc[j]);
         }
       // issue order: every read, then the rank MFMAs, then (after the
       // scaling) the head-dim MFMAs of S and dP.  With two key slices the
@@ -491,7 +496,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       const bool diag = p.causal && x.k0t + (kw * C::KPW + ks) * 32 + 31 > qbase;  // wave-uniform
       const int thr = x.k0t + krow_of(ks) - qbase;
       auto body = [&](auto masked) {
-        u32x4 pk[2], dk[2];
+        u32x4 pk[2], dk[2], dr[2];
 #pragma unroll
         for (int gq = 0; gq < 4; ++gq) {
           const int r0 = 8 * gq + 4 * hl;
@@ -508,16 +513,24 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
               pv[j] = e;
             dv[j] = pv[j] * (dpacc[v] - dl4[j]);
           }
-          pk[gq >> 1][2 * (gq & 1)] = pack_bf16(pv[0], pv[1]);
-          pk[gq >> 1][2 * (gq & 1) + 1] = pack_bf16(pv[2], pv[3]);
-          dk[gq >> 1][2 * (gq & 1)] = pack_bf16(dv[0], dv[1]);
-          dk[gq >> 1][2 * (gq & 1) + 1] = pack_bf16(dv[2], dv[3]);
+          pk[gq >> 1][2 * (gq & 1)] = pack_e<F16>(pv[0], pv[1]);
+          pk[gq >> 1][2 * (gq & 1) + 1] = pack_e<F16>(pv[2], pv[3]);
+          dk[gq >> 1][2 * (gq & 1)] = pack_e<F16>(dv[0], dv[1]);
+          dk[gq >> 1][2 * (gq & 1) + 1] = pack_e<F16>(dv[2], dv[3]);
+          if constexpr (C::DBR) {
+            dr[gq >> 1][2 * (gq & 1)] = pack_bf16(dv[0], dv[1]);
+            dr[gq >> 1][2 * (gq & 1) + 1] = pack_bf16(dv[2], dv[3]);
+          }
         }
-        uint8_t* o = pd + kw * C::PW + ks * 4096 + lane * 16;
+        uint8_t* o = pd + kw * C::PW + ks * C::SL + lane * 16;
         st16(o, pk[0]);
         st16(o + 1024, pk[1]);
         st16(o + 2048, dk[0]);
         st16(o + 3072, dk[1]);
+        if constexpr (C::DBR) {
+          st16(o + 4096, dr[0]);
+          st16(o + 5120, dr[1]);
+        }
       };
       if (diag)
         body(std::true_type{});
@@ -632,8 +645,11 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     // in accumulator tile t; one exchange between the lane halves per
     // register pair (i = 2 u, 2 u + 1) gives each lane 8 consecutive
     // features: 32 t + 16 u + 8 hl .. +7, in the returned order.
-    auto swap8 = [&](const f32x16& a, float sc, bool zero, int u) {
-      auto pk = [&](int v) { return zero ? 0u : pack_bf16(sc * a[v], sc * a[v + 1]); };
+    // (f16: std::bool_constant, rounding to fp16 rather than bf16)
+    auto swap8 = [&](const f32x16& a, float sc, bool zero, int u, auto f16) {
+      auto pk = [&](int v) {
+        return zero ? 0u : pack_e<decltype(f16)::value>(sc * a[v], sc * a[v + 1]);
+      };
       const auto lo = __builtin_amdgcn_permlane32_swap(pk(8 * u), pk(8 * u + 4), false, false);
       const auto hi = __builtin_amdgcn_permlane32_swap(pk(8 * u + 2), pk(8 * u + 6), false, false);
       return u32x4{lo[0], hi[0], lo[1], hi[1]};
@@ -648,7 +664,8 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
 #pragma unroll
             for (int f = 0; f < C::NRB; ++f)
 #pragma unroll
-              for (int u = 0; u < 2; ++u) w[f][u] = swap8(dkacc[j][C::NDB + f], sr, zero, u);
+              for (int u = 0; u < 2; ++u)
+                w[f][u] = swap8(dkacc[j][C::NDB + f], sr, zero, u, std::false_type{});
             const int key = x.k0t + krow_of(j);
             if (key < x.e.lk) {
               const TView vd = view_of(&params_here()->drk);
@@ -673,7 +690,7 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
 #pragma unroll
       for (int t = 0; t < C::NDB; ++t)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) w[t][u] = swap8(acc[t], sc, zero, u);
+        for (int u = 0; u < 2; ++u) w[t][u] = swap8(acc[t], sc, zero, u, std::bool_constant<F16>{});
       const int key = x.k0t + krow_of(j);
       if (key < x.e.lk) {
         uint16_t* rp = seq_base<uint16_t>(out, p, x.b, x.e.k0, x.kvh) + (int64_t)key * out.ss + 8 * hl;
@@ -762,52 +779,61 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
       // Every transposed operand read serves the wave's KPW key slices.  One
       // slice reads its P and dS operands first; two read them one k-half
       // at a time (registers).
-      auto mfmas = [&](int j, const bf16x8* pbj, const bf16x8* dbj) {
+      // (dbrj: dS in bf16 for the dRk chain, where it differs from dbj)
+      auto mfmas = [&](int j, const bf16x8* pbj, const bf16x8* dbj, const bf16x8* dbrj) {
 #pragma unroll
         for (int d = 0; d < C::NDB; ++d) {
           const bf16x8 a = tr_operand<C::BM>(ot, tl, 16 * j, 32 * d);
 #pragma unroll
-          for (int ks = 0; ks < C::KPW; ++ks) dvacc[ks][d] = mfma32(a, pbj[ks], dvacc[ks][d]);
+          for (int ks = 0; ks < C::KPW; ++ks)
+            dvacc[ks][d] = mfma_e<F16>(a, pbj[ks], dvacc[ks][d]);
         }
 #pragma unroll
         for (int d = 0; d < C::NDB; ++d) {
           const bf16x8 a = tr_operand<C::BM>(qt, tl, 16 * j, 32 * d);
 #pragma unroll
-          for (int ks = 0; ks < C::KPW; ++ks) dkacc[ks][d] = mfma32(a, dbj[ks], dkacc[ks][d]);
+          for (int ks = 0; ks < C::KPW; ++ks)
+            dkacc[ks][d] = mfma_e<F16>(a, dbj[ks], dkacc[ks][d]);
         }
 #pragma unroll
         for (int f = 0; f < C::NRB; ++f) {
           const bf16x8 a = tr_operand<C::BM>(rt, tl, 16 * j, 32 * f);
 #pragma unroll
           for (int ks = 0; ks < C::KPW; ++ks)
-            dkacc[ks][C::NDB + f] = mfma32(a, dbj[ks], dkacc[ks][C::NDB + f]);
+            dkacc[ks][C::NDB + f] = mfma32(a, dbrj[ks], dkacc[ks][C::NDB + f]);
         }
       };
       const uint8_t* o = pd + kw * C::PW + lane * 16;
+      constexpr int NPD = C::DBR ? 3 : 2;  // operand reads per k-half and slice
       if constexpr (C::KPW == 1) {
-        bf16x8 pb[2][1], db[2][1];
+        bf16x8 pb[2][1], db[2][1], dbr[2][1];
         pb[0][0] = as_bf16x8(ld16(o));
         pb[1][0] = as_bf16x8(ld16(o + 1024));
         db[0][0] = as_bf16x8(ld16(o + 2048));
         db[1][0] = as_bf16x8(ld16(o + 3072));
-        mfmas(0, pb[0], db[0]);
-        mfmas(1, pb[1], db[1]);
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        if constexpr (C::DBR) {
+          dbr[0][0] = as_bf16x8(ld16(o + 4096));
+          dbr[1][0] = as_bf16x8(ld16(o + 5120));
+        }
+        mfmas(0, pb[0], db[0], C::DBR ? dbr[0] : db[0]);
+        mfmas(1, pb[1], db[1], C::DBR ? dbr[1] : db[1]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * NPD, 0);
         pipe_lds_mfma<2 * (2 * C::NDB + C::NRB), 2, 3>();
       } else {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          bf16x8 pbj[C::KPW], dbj[C::KPW];
+          bf16x8 pbj[C::KPW], dbj[C::KPW], dbrj[C::KPW];
 #pragma unroll
           for (int ks = 0; ks < C::KPW; ++ks) {
-            pbj[ks] = as_bf16x8(ld16(o + ks * 4096 + j * 1024));
-            dbj[ks] = as_bf16x8(ld16(o + ks * 4096 + 2048 + j * 1024));
+            pbj[ks] = as_bf16x8(ld16(o + ks * C::SL + j * 1024));
+            dbj[ks] = as_bf16x8(ld16(o + ks * C::SL + 2048 + j * 1024));
+            if constexpr (C::DBR) dbrj[ks] = as_bf16x8(ld16(o + ks * C::SL + 4096 + j * 1024));
           }
-          mfmas(j, pbj, dbj);
+          mfmas(j, pbj, dbj, C::DBR ? dbrj : dbj);
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 2 * C::KPW, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, NPD * C::KPW, 0);
           pipe_lds_mfma<2 * C::NDB + C::NRB, 2, 2, C::KPW>();
         }
       }
@@ -920,10 +946,15 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
   }
 }
 
-// One non-template kernel per (D, padded rank) so that each has a host stub.
-#define FNA2_DKDV_KERNEL(D, RPL)                                                      \
+// One non-template kernel per (D, padded rank, element type) so that each
+// has a host stub.
+#define FNA2_DKDV_KERNEL(D, RPL)                                                       \
   __global__ __launch_bounds__(512, 1) void dkdv_kernel_d##D##_r##RPL(const BwdParams P) { \
-    dkdv_body<D, RPL>(P);                                                             \
+    dkdv_body<D, RPL, false>(P);                                                       \
+  }                                                                                    \
+  __global__ __launch_bounds__(512, 1) void dkdv_kernel_d##D##_r##RPL##_f16(             \
+      const BwdParams P) {                                                             \
+    dkdv_body<D, RPL, true>(P);                                                        \
   }
 FNA2_DKDV_KERNEL(64, 0)
 FNA2_DKDV_KERNEL(64, 32)
@@ -938,10 +969,19 @@ FNA2_DKDV_KERNEL(128, 64)
 hipError_t launch_bwd_dkdv(const BwdParams& P, int rpl, int grid, hipStream_t s) {
   if (grid <= 0) return hipSuccess;
   void (*k)(const BwdParams) = nullptr;
-  if (P.p.D == 64)
-    k = rpl == 0 ? dkdv_kernel_d64_r0 : rpl == 32 ? dkdv_kernel_d64_r32 : dkdv_kernel_d64_r64;
-  if (P.p.D == 128)
-    k = rpl == 0 ? dkdv_kernel_d128_r0 : rpl == 32 ? dkdv_kernel_d128_r32 : dkdv_kernel_d128_r64;
+  if (P.p.f16) {
+    if (P.p.D == 64)
+      k = rpl == 0 ? dkdv_kernel_d64_r0_f16
+                   : rpl == 32 ? dkdv_kernel_d64_r32_f16 : dkdv_kernel_d64_r64_f16;
+    if (P.p.D == 128)
+      k = rpl == 0 ? dkdv_kernel_d128_r0_f16
+                   : rpl == 32 ? dkdv_kernel_d128_r32_f16 : dkdv_kernel_d128_r64_f16;
+  } else {
+    if (P.p.D == 64)
+      k = rpl == 0 ? dkdv_kernel_d64_r0 : rpl == 32 ? dkdv_kernel_d64_r32 : dkdv_kernel_d64_r64;
+    if (P.p.D == 128)
+      k = rpl == 0 ? dkdv_kernel_d128_r0 : rpl == 32 ? dkdv_kernel_d128_r32 : dkdv_kernel_d128_r64;
+  }
   if (!k || (rpl != 0 && rpl != 32 && rpl != 64)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k, dim3(grid), dim3(512), 0, s, P);
   return hipGetLastError();

@@ -73,7 +73,7 @@ __device__ void zero_uncovered_rows(const BwdParams& P, int w, int nw) {
   }
 }
 
-template <int D, int RPL>
+template <int D, int RPL, bool F16>
 __device__ __forceinline__ void dq_body(const BwdParams& P) {
   using C = DqCfg<D, RPL>;
   __shared__ __attribute__((aligned(1024))) uint8_t st0[C::STAGE];
@@ -212,7 +212,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
         const u32x4 o = as_u32x4(oreg[s]);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          dl += bf16_lo(y[i]) * bf16_lo(o[i]) + bf16_hi(y[i]) * bf16_hi(o[i]);
+          dl += elt_lo<F16>(y[i]) * elt_lo<F16>(o[i]) + elt_hi<F16>(y[i]) * elt_hi<F16>(o[i]);
       }
       dl += __shfl_xor(dl, 32);
     }
@@ -236,7 +236,12 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
     const uint8_t* kt = cur;
     const uint8_t* rt = cur + C::KB;
     const uint8_t* vt = cur + C::KB + C::RB;
+    // dS^T as B operands: in the element type for the dQ chain (K^T is of
+    // that type) and in bf16 for the dRq chain (Rk^T is bf16); one array
+    // when the two types agree.
+    constexpr bool DBR = F16 && C::NRB > 0;
     bf16x8 db[C::NKB][2];
+    bf16x8 dbr[DBR ? C::NKB : 1][2];
 #pragma unroll
     for (int kb2 = 0; kb2 < C::NKB; ++kb2) {
       // S^T / c = b Rk Rq^T + K (a Q)^T: the rank chain, scaled by b in
@@ -249,9 +254,11 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
         sacc *= bh;
       }
 #pragma unroll
-      for (int s = 0; s < C::KSD; ++s) sacc = mfma32(row_read<C::BN>(kt, rdl, kb2 * 32, s), qreg[s], sacc);
+      for (int s = 0; s < C::KSD; ++s)
+        sacc = mfma_e<F16>(row_read<C::BN>(kt, rdl, kb2 * 32, s), qreg[s], sacc);
 #pragma unroll
-      for (int s = 0; s < C::KSD; ++s) dpacc = mfma32(row_read<C::BN>(vt, rdl, kb2 * 32, s), oreg[s], dpacc);
+      for (int s = 0; s < C::KSD; ++s)
+        dpacc = mfma_e<F16>(row_read<C::BN>(vt, rdl, kb2 * 32, s), oreg[s], dpacc);
       // dS^T = P^T (dP^T - delta).  Zero-filled key rows (past the
       // sequence) and query rows give K = Rk = 0 or dO = 0 and contribute
       // nothing, so only the causal diagonal needs a mask.
@@ -264,7 +271,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
       }
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        u32x4 dk4;
+        u32x4 dk4, dr4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float dv2[2];
@@ -274,9 +281,11 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
             const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[v], p.c2, -lse2));
             dv2[j] = pr * (dpacc[v] - dl);
           }
-          dk4[i] = pack_bf16(dv2[0], dv2[1]);
+          dk4[i] = pack_e<F16>(dv2[0], dv2[1]);
+          if constexpr (DBR) dr4[i] = pack_bf16(dv2[0], dv2[1]);
         }
         db[kb2][half] = as_bf16x8(dk4);
+        if constexpr (DBR) dbr[kb2][half] = as_bf16x8(dr4);
       }
     }
     // dQa^T += Ka^T dA^T
@@ -287,13 +296,14 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
         const int k0 = kb2 * 32 + 16 * half;
 #pragma unroll
         for (int f = 0; f < C::NDB; ++f)
-          acc[f] = mfma32(tr_operand<C::BN>(kt, tl, k0, 32 * f), db[kb2][half], acc[f]);
+          acc[f] = mfma_e<F16>(tr_operand<C::BN>(kt, tl, k0, 32 * f), db[kb2][half], acc[f]);
         if constexpr (C::NRB > 0) {
           if (graph) {
 #pragma unroll
             for (int f = 0; f < C::NRB; ++f)
-              acc[C::NDB + f] =
-                  mfma32(tr_operand<C::BN>(rt, tl, k0, 32 * f), db[kb2][half], acc[C::NDB + f]);
+              acc[C::NDB + f] = mfma32(tr_operand<C::BN>(rt, tl, k0, 32 * f),
+                                       DBR ? dbr[DBR ? kb2 : 0][half] : db[kb2][half],
+                                       acc[C::NDB + f]);
           }
         }
       }
@@ -356,8 +366,9 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
   for (int d = 0; d < C::NDB; ++d)
 #pragma unroll
     for (int g = 0; g < 4; ++g)
-      QS::put4(obuf, l32, d * 32 + 8 * g + 4 * hl, sq * acc[d][4 * g], sq * acc[d][4 * g + 1],
-               sq * acc[d][4 * g + 2], sq * acc[d][4 * g + 3]);
+      QS::template put4<F16>(obuf, l32, d * 32 + 8 * g + 4 * hl, sq * acc[d][4 * g],
+                             sq * acc[d][4 * g + 1], sq * acc[d][4 * g + 2],
+                             sq * acc[d][4 * g + 3]);
   QS::store(obuf, seq_base<uint16_t>(P.dq, p, b, e.q0, h) + (int64_t)wq0 * P.dq.ss, P.dq.ss,
             nrows, QS::CPR, lane);
   if constexpr (C::NRB > 0) {
@@ -407,9 +418,13 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
 }
 
 // WAVES: waves per SIMD the register budget is cut for.
-#define FNA2_DQ_KERNEL(D, RPL, WAVES)                                                   \
+#define FNA2_DQ_KERNEL(D, RPL, WAVES)                                                    \
   __global__ __launch_bounds__(256, WAVES) void dq_kernel_d##D##_r##RPL(const BwdParams P) { \
-    dq_body<D, RPL>(P);                                                                 \
+    dq_body<D, RPL, false>(P);                                                           \
+  }                                                                                      \
+  __global__ __launch_bounds__(256, WAVES) void dq_kernel_d##D##_r##RPL##_f16(             \
+      const BwdParams P) {                                                               \
+    dq_body<D, RPL, true>(P);                                                            \
   }
 FNA2_DQ_KERNEL(64, 0, 3)
 FNA2_DQ_KERNEL(64, 32, 3)
@@ -424,9 +439,16 @@ FNA2_DQ_KERNEL(128, 64, 2)
 hipError_t launch_bwd_dq(const BwdParams& P, int rpl, int grid, hipStream_t s) {
   if (grid <= 0) return hipSuccess;
   void (*k)(const BwdParams) = nullptr;
-  if (P.p.D == 64) k = rpl == 0 ? dq_kernel_d64_r0 : rpl == 32 ? dq_kernel_d64_r32 : dq_kernel_d64_r64;
-  if (P.p.D == 128)
-    k = rpl == 0 ? dq_kernel_d128_r0 : rpl == 32 ? dq_kernel_d128_r32 : dq_kernel_d128_r64;
+  if (P.p.f16) {
+    if (P.p.D == 64)
+      k = rpl == 0 ? dq_kernel_d64_r0_f16 : rpl == 32 ? dq_kernel_d64_r32_f16 : dq_kernel_d64_r64_f16;
+    if (P.p.D == 128)
+      k = rpl == 0 ? dq_kernel_d128_r0_f16 : rpl == 32 ? dq_kernel_d128_r32_f16 : dq_kernel_d128_r64_f16;
+  } else {
+    if (P.p.D == 64) k = rpl == 0 ? dq_kernel_d64_r0 : rpl == 32 ? dq_kernel_d64_r32 : dq_kernel_d64_r64;
+    if (P.p.D == 128)
+      k = rpl == 0 ? dq_kernel_d128_r0 : rpl == 32 ? dq_kernel_d128_r32 : dq_kernel_d128_r64;
+  }
   if (!k || (rpl != 0 && rpl != 32 && rpl != 64)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k, dim3(grid), dim3(256), 0, s, P);
   return hipGetLastError();

@@ -38,7 +38,7 @@ int64_t rows_k(const fna2_problem& p) {
 }
 
 int check_problem(const fna2_problem& p) {
-  if (p.dtype != FNA2_BF16) return FNA2_E_DTYPE;
+  if (p.dtype != FNA2_BF16 && p.dtype != FNA2_F16) return FNA2_E_DTYPE;
   if (p.head_dim != 64 && p.head_dim != 128) return FNA2_E_HEAD_DIM;
   if (p.heads <= 0 || p.heads_kv <= 0 || p.heads % p.heads_kv != 0) return FNA2_E_HEADS;
   if (p.heads_graph < 0 || p.heads_graph > p.heads) return FNA2_E_HEADS;
@@ -195,12 +195,15 @@ bool use_plan(const void* plan, const fna2_problem& p) { return plan && p.varlen
 // counts and lists sized by its sequence count, so a backward may only read
 // a plan built for the same sequences: fna2_bwd uses a plan found here with
 // a matching key, and otherwise builds its own lists (as without a plan).
-// A small ring: an address reused by a later forward is re-registered.
+// A small ring: an address reused by a later forward is re-registered.  The
+// key-tile size (head_dim and padded rank pick it) shapes the key list, so
+// it is part of the key: a plan built for another tile size is not used.
 uint64_t plan_key(const fna2_problem& p) {
   const uint64_t f[] = {(uint64_t)p.batch,          (uint64_t)p.total_q,
                         (uint64_t)p.total_k,        (uint64_t)p.causal,
                         (uint64_t)(uintptr_t)p.cu_seqlens_q,
-                        (uint64_t)(uintptr_t)p.cu_seqlens_k};
+                        (uint64_t)(uintptr_t)p.cu_seqlens_k,
+                        (uint64_t)kv_tile(p)};
   uint64_t h = 1469598103934665603ull;  // FNV-1a over the words
   for (uint64_t w : f) {
     for (int i = 0; i < 8; ++i) {
@@ -255,6 +258,7 @@ fna2::Problem make_problem(const fna2_problem& p) {
   P.D = p.head_dim;
   P.R = p.heads_graph > 0 ? p.rank : 0;
   P.causal = p.causal ? 1 : 0;
+  P.f16 = p.dtype == FNA2_F16 ? 1 : 0;
   P.group = p.heads / p.heads_kv;
   const float s = p.softmax_scale;
   if (s > 0.f) {
@@ -318,7 +322,7 @@ const char* fna2_status_string(int s) {
   switch (s) {
     case FNA2_OK: return "ok";
     case FNA2_E_NULL: return "a required pointer is NULL";
-    case FNA2_E_DTYPE: return "unsupported dtype (attention: bf16 only)";
+    case FNA2_E_DTYPE: return "unsupported dtype (attention: bf16 or fp16)";
     case FNA2_E_HEAD_DIM: return "head_dim must be 64 or 128";
     case FNA2_E_RANK: return "rank must be a multiple of 8 in [8, 64]";
     case FNA2_E_HEADS: return "heads must be a multiple of heads_kv and heads_graph <= heads";

@@ -55,6 +55,7 @@ struct Problem {
   int total_q, total_k;
   int H, H_KV, H_G, D, R;
   int causal;
+  int f16;         // head-dim tensors are fp16 (else bf16); picks the kernel
   int group;       // H / H_KV
   float c;         // positive score multiplier
   float c2;        // c * log2(e)
@@ -167,6 +168,25 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// Element type of the head-dim tensors (q, k, v, out, dout, dq, dk, dv):
+// bf16, or fp16 where a kernel is instantiated with F16.  R_q, R_k and their
+// gradients are bf16 in both, as the reference asserts
+// (FNA2/flash_naylis_attn.py:1419-1420): the rank chain of the augmented
+// contraction always runs on the bf16 MFMA, the head-dim chain and the P / dS
+// products on the one of the element type, accumulating into the same fp32
+// registers.  Operands travel as 16-byte bit patterns typed bf16x8.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+template <bool F16>
+__device__ __forceinline__ f32x16 mfma_e(bf16x8 a, bf16x8 b, f32x16 c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {
   return __builtin_bit_cast(bf16x8, v);
 }
@@ -186,6 +206,34 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   f32x2 x = {lo, hi};
   bf16x2 y = __builtin_convertvector(x, bf16x2);
   return __builtin_bit_cast(uint32_t, y);
+}
+
+// Round two floats to the element type (RNE) and pack: lo in bits 0..15.
+template <bool F16>
+__device__ __forceinline__ uint32_t pack_e(float lo, float hi) {
+  if constexpr (F16) {
+    f32x2 x = {lo, hi};
+    f16x2 y = __builtin_convertvector(x, f16x2);
+    return __builtin_bit_cast(uint32_t, y);
+  } else {
+    return pack_bf16(lo, hi);
+  }
+}
+
+// The two element-type values of a packed word, as floats.
+template <bool F16>
+__device__ __forceinline__ float elt_lo(uint32_t w) {
+  if constexpr (F16)
+    return (float)__builtin_bit_cast(f16x2, w)[0];
+  else
+    return __builtin_bit_cast(float, w << 16);
+}
+template <bool F16>
+__device__ __forceinline__ float elt_hi(uint32_t w) {
+  if constexpr (F16)
+    return (float)__builtin_bit_cast(f16x2, w)[1];
+  else
+    return __builtin_bit_cast(float, w & 0xffff0000u);
 }
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) {

@@ -10,8 +10,9 @@
 // one MFMA chain over the augmented width D + R (the bias is fused into the
 // same contraction), so
 // each lane holds one query column and the row softmax needs one exchange
-// (lane ^ 32).  The bf16 probabilities are the B operand of
-// O^T += V^T P^T straight from the accumulator registers; V^T comes from
+// (lane ^ 32).  The probabilities, rounded to the element type (bf16, or
+// fp16 for fp16 q/k/v, as the reference's p.to(v.dtype), :187), are the B
+// operand of O^T += V^T P^T straight from the accumulator registers; V^T comes from
 // the row-major V tile through ds_read_b64_tr_b16.  K, Rk and V tiles are
 // DMA'd global -> LDS (buffer_load ... lds, zero-filled past the sequence)
 // into a two-stage ring: the next tile streams in while this one computes.
@@ -41,7 +42,7 @@ struct FwdCfg {
   static constexpr int STAGE = KBYTES + RBYTES + VBYTES;
 };
 
-template <int D, int RPL>
+template <int D, int RPL, bool F16>
 __device__ __forceinline__ void fwd_body(const FwdParams& P) {
   using C = FwdCfg<D, RPL>;
   // Two stages as separate objects: the compiler can then tell that reads of
@@ -175,7 +176,8 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
         acc *= bh;
       }
 #pragma unroll
-      for (int s = 0; s < C::KSD; ++s) acc = mfma32(row_read<C::BN>(kl, rdl, kb2 * 32, s), qreg[s], acc);
+      for (int s = 0; s < C::KSD; ++s)
+        acc = mfma_e<F16>(row_read<C::BN>(kl, rdl, kb2 * 32, s), qreg[s], acc);
       sacc[kb2] = acc;
     }
     if ((kbase + C::BN > e.lk) || (p.causal && kbase + C::BN - 1 > wq0)) {
@@ -222,7 +224,7 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
           const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb2][v0], p.c2, nm));
           const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb2][v0 + 1], p.c2, nm));
           ls += p0 + p1;
-          pk[i] = pack_bf16(p0, p1);
+          pk[i] = pack_e<F16>(p0, p1);
         }
         pb[kb2 * 2 + half] = as_bf16x8(pk);
       }
@@ -232,7 +234,7 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
     for (int s = 0; s < C::BN / 16; ++s)
 #pragma unroll
       for (int d = 0; d < D / 32; ++d)
-        oacc[d] = mfma32(tr_operand<C::BN>(vl, tl, 16 * s, 32 * d), pb[s], oacc[d]);
+        oacc[d] = mfma_e<F16>(tr_operand<C::BN>(vl, tl, 16 * s, 32 * d), pb[s], oacc[d]);
   };
 
   for (int kt = 0; kt < nkv; kt += 2) {
@@ -256,7 +258,7 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
     for (int d = 0; d < D / 32; ++d)
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-        OS::put4(obuf, l32, d * 32 + 8 * g + 4 * hl, oacc[d][4 * g] * inv,
+        OS::template put4<F16>(obuf, l32, d * 32 + 8 * g + 4 * hl, oacc[d][4 * g] * inv,
                  oacc[d][4 * g + 1] * inv, oacc[d][4 * g + 2] * inv, oacc[d][4 * g + 3] * inv);
     OS::store(obuf, seq_base<uint16_t>(P.o, p, b, e.q0, h) + (int64_t)wq0 * P.o.ss, P.o.ss,
               max(min(32, e.lq - wq0), 0), OS::CPR, lane);
@@ -269,8 +271,8 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         u32x2 val;
-        val[0] = pack_bf16(oacc[d][4 * g] * inv, oacc[d][4 * g + 1] * inv);
-        val[1] = pack_bf16(oacc[d][4 * g + 2] * inv, oacc[d][4 * g + 3] * inv);
+        val[0] = pack_e<F16>(oacc[d][4 * g] * inv, oacc[d][4 * g + 1] * inv);
+        val[1] = pack_e<F16>(oacc[d][4 * g + 2] * inv, oacc[d][4 * g + 3] * inv);
         *(u32x2*)(orow + d * 32 + 8 * g + 4 * hl) = val;
       }
   }
@@ -282,11 +284,16 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
   }
 }
 
-// One non-template kernel per (D, padded rank): every kernel gets its own
-// host launch stub.  WAVES: waves per SIMD the register budget is cut for.
-#define FNA2_FWD_KERNEL(D, RPL, WAVES)                                                     \
+// One non-template kernel per (D, padded rank, element type): every kernel
+// gets its own host launch stub.  WAVES: waves per SIMD the register budget
+// is cut for.
+#define FNA2_FWD_KERNEL(D, RPL, WAVES)                                                      \
   __global__ __launch_bounds__(256, WAVES) void fwd_kernel_d##D##_r##RPL(const FwdParams P) { \
-    fwd_body<D, RPL>(P);                                                                   \
+    fwd_body<D, RPL, false>(P);                                                             \
+  }                                                                                         \
+  __global__ __launch_bounds__(256, WAVES) void fwd_kernel_d##D##_r##RPL##_f16(               \
+      const FwdParams P) {                                                                  \
+    fwd_body<D, RPL, true>(P);                                                              \
   }
 FNA2_FWD_KERNEL(64, 0, 2)
 FNA2_FWD_KERNEL(64, 32, 2)
@@ -301,8 +308,15 @@ FNA2_FWD_KERNEL(128, 64, 3)
 hipError_t launch_fwd(const FwdParams& P, int rpl, int grid, hipStream_t s) {
   if (grid <= 0) return hipSuccess;
   void (*k)(const FwdParams) = nullptr;
-  if (P.p.D == 64) k = rpl == 0 ? fwd_kernel_d64_r0 : rpl == 32 ? fwd_kernel_d64_r32 : fwd_kernel_d64_r64;
-  if (P.p.D == 128) k = rpl == 0 ? fwd_kernel_d128_r0 : rpl == 32 ? fwd_kernel_d128_r32 : fwd_kernel_d128_r64;
+  if (P.p.f16) {
+    if (P.p.D == 64)
+      k = rpl == 0 ? fwd_kernel_d64_r0_f16 : rpl == 32 ? fwd_kernel_d64_r32_f16 : fwd_kernel_d64_r64_f16;
+    if (P.p.D == 128)
+      k = rpl == 0 ? fwd_kernel_d128_r0_f16 : rpl == 32 ? fwd_kernel_d128_r32_f16 : fwd_kernel_d128_r64_f16;
+  } else {
+    if (P.p.D == 64) k = rpl == 0 ? fwd_kernel_d64_r0 : rpl == 32 ? fwd_kernel_d64_r32 : fwd_kernel_d64_r64;
+    if (P.p.D == 128) k = rpl == 0 ? fwd_kernel_d128_r0 : rpl == 32 ? fwd_kernel_d128_r32 : fwd_kernel_d128_r64;
+  }
   if (!k || (rpl != 0 && rpl != 32 && rpl != 64)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k, dim3(grid), dim3(256), 0, s, P);
   return hipGetLastError();

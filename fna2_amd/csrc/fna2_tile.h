@@ -258,8 +258,8 @@ __device__ __forceinline__ bf16x8 tr_operand(const uint8_t* tile, const TrLane& 
   return __builtin_bit_cast(bf16x8, ab);
 }
 
-// Epilogue staging of a wave's 32 output rows of W bf16 values (W = 32, 64
-// or 128) in LDS, so that global stores write whole rows.  The accumulators
+// Epilogue staging of a wave's 32 output rows of W 16-bit values (W = 32,
+// 64 or 128) in LDS, so that global stores write whole rows.  The accumulators
 // hold, per lane, 4 consecutive values of one row (row = lane % 32), so a
 // staging write is an 8-byte write by 32 rows x 2 halves of one 16-byte
 // chunk, and a store reads whole chunks (ds_read_b128) of RPI rows.  Row r
@@ -292,12 +292,14 @@ struct RowStage {
   __device__ __forceinline__ static int off(int row, int col) {
     return row * W * 2 + (pos(row, col >> 3) << 4) + ((((col >> 2) & 1) ^ hswap(row)) << 3);
   }
-  // 4 values (col a multiple of 4) of row `row`.
+  // 4 values (col a multiple of 4) of row `row`, rounded to bf16 (fp16
+  // with F16).
+  template <bool F16 = false>
   __device__ __forceinline__ static void put4(uint8_t* buf, int row, int col, float a, float b,
                                               float c, float d) {
     u32x2 v;
-    v[0] = pack_bf16(a, b);
-    v[1] = pack_bf16(c, d);
+    v[0] = pack_e<F16>(a, b);
+    v[1] = pack_e<F16>(c, d);
     *(u32x2*)(buf + off(row, col)) = v;
   }
   // Stores rows [0, nrows) to dst + row * stride (elements), chunks [0,

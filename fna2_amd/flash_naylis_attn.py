@@ -29,7 +29,9 @@ Differences from the reference, all supersets:
   atomics, :546-553) and bitwise reproducible.
 
 Tensors need a unit innermost stride and 16-byte aligned rows; other layouts
-are copied with ``.contiguous()`` first.  Inputs must be bfloat16.
+are copied with ``.contiguous()`` first.  q, k and v are bfloat16 or float16
+(one dtype; out and dq / dk / dv take it), r_q and r_k bfloat16, as in the
+reference.
 """
 from __future__ import annotations
 
@@ -47,6 +49,7 @@ BLOCK_N = 64   # keys per forward step
 BLOCK_R = 32   # default rel_rank (NaylisAttention's default)
 
 SUPPORTED_HEAD_DIMS = (64, 128)
+SUPPORTED_DTYPES = (torch.bfloat16, torch.float16)  # q, k, v (r_q / r_k: bfloat16)
 SUPPORTED_RANKS = tuple(range(8, 65, 8))
 
 
@@ -101,8 +104,12 @@ def _stream(dev: torch.device) -> int:
 
 
 def _check_inputs(q, k, v, r_q, r_k, graph_scale):
+    # q, k, v: bf16 or fp16, one dtype (the reference's kernels are generic
+    # over it, FNA2/flash_naylis_attn.py:187, :201, :522-529); r_q, r_k: bf16
+    # (:1419-1420).
+    assert q.dtype in SUPPORTED_DTYPES, f"q must be bfloat16 or float16 (got {q.dtype})"
     for name, t in (("q", q), ("k", k), ("v", v)):
-        assert t.dtype == torch.bfloat16, f"{name} must be bfloat16 (got {t.dtype})"
+        assert t.dtype == q.dtype, f"{name} must have q's dtype {q.dtype} (got {t.dtype})"
         assert t.is_cuda, f"{name} must be a GPU tensor"
     if r_q is not None:
         assert r_k is not None, "r_q and r_k must both be given"
@@ -122,8 +129,9 @@ def _gs32(graph_scale: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
 
 
 def _problem(varlen, batch, sq, sk, tq, tk, H, H_KV, H_G, D, R, causal, scale, cu_q=None,
-             cu_k=None) -> _capi.Problem:
-    return _capi.Problem(_capi.FNA2_BF16, int(varlen), int(batch), int(sq), int(sk), int(tq),
+             cu_k=None, dtype=torch.bfloat16) -> _capi.Problem:
+    code = _capi.FNA2_F16 if dtype == torch.float16 else _capi.FNA2_BF16
+    return _capi.Problem(code, int(varlen), int(batch), int(sq), int(sk), int(tq),
                          int(tk), int(H), int(H_KV), int(H_G), int(D), int(R), int(bool(causal)),
                          float(scale), _ptr(cu_q), _ptr(cu_k))
 
@@ -260,7 +268,8 @@ def _fna2_forward(
     gs = _gs32(graph_scale) if H_G else None
     out = torch.empty_like(q)
     lse = torch.empty(B, H, S, device=q.device, dtype=torch.float32)
-    prob = _problem(False, B, S, S_k, 0, 0, H, H_KV, H_G, D, R, is_causal, softmax_scale)
+    prob = _problem(False, B, S, S_k, 0, 0, H, H_KV, H_G, D, R, is_causal, softmax_scale,
+                    dtype=q.dtype)
     _run_fwd(prob, q, k, v, r_q if H_G else None, r_k if H_G else None, gs, out, lse, _view4)
     return out, lse
 
@@ -279,10 +288,18 @@ def _fna2_forward_varlen(
     softmax_scale: float,
     is_causal: bool = True,
     plan: Optional[torch.Tensor] = None,
+    lse_head_major: bool = False,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Varlen forward; returns (out [T,H,D], lse [T,H]).  Mirrors :756-804.
     ``plan`` (from ``new_plan``, optional): also build the backward's tile
-    lists into it, for an ``_fna2_backward_varlen`` given the same plan."""
+    lists into it, for an ``_fna2_backward_varlen`` given the same plan.
+
+    ``lse`` is a contiguous ``[T, H]`` tensor, as the reference allocates it
+    (:780).  ``lse_head_major=True`` (the autograd and custom-operator paths)
+    returns the same values as a ``[T, H]`` view of head-major ``[H, T]``
+    memory instead: a forward workgroup's 128 rows of one head are then one
+    contiguous run (row-major ``[T, H]`` puts each 4-byte value in its own
+    64-byte segment: 75.9 MB written per c3 forward against 68.2)."""
     total_q, H, D = q.shape
     total_k, H_KV = k.shape[0], k.shape[1]
     H_G = 0 if r_q is None else r_q.shape[1]
@@ -301,12 +318,12 @@ def _fna2_forward_varlen(
     cu_k = cu_seqlens_k.to(device=q.device, dtype=torch.int32).contiguous()
     gs = _gs32(graph_scale) if H_G else None
     out = torch.empty_like(q)
-    # [T, H] as the reference returns it, viewing head-major memory: a
-    # workgroup's 128 rows of one head are then one contiguous run (row-major
-    # [T, H] put each 4-byte value in its own 64-byte segment).
-    lse = torch.empty(H, total_q, device=q.device, dtype=torch.float32).t()
+    if lse_head_major:
+        lse = torch.empty(H, total_q, device=q.device, dtype=torch.float32).t()
+    else:
+        lse = torch.empty(total_q, H, device=q.device, dtype=torch.float32)
     prob = _problem(True, N, max_seqlen_q, max_seqlen_k, total_q, total_k, H, H_KV, H_G, D, R,
-                    is_causal, softmax_scale, cu_q, cu_k)
+                    is_causal, softmax_scale, cu_q, cu_k, dtype=q.dtype)
     _run_fwd(prob, q, k, v, r_q if H_G else None, r_k if H_G else None, gs, out, lse, _view3,
              plan)
     return out, lse
@@ -333,14 +350,15 @@ def _fna2_backward(
     H_KV, S_k = k.shape[1], k.shape[2]
     H_G = 0 if r_q is None else r_q.shape[1]
     R = 0 if r_q is None else r_q.shape[3]
-    dout = _prep(dout)
+    dout = _prep(dout if dout.dtype == q.dtype else dout.to(q.dtype))  # as do.to(v.dtype), :522
     q, k, v, r_q, r_k, out = (_prep(t) for t in (q, k, v, r_q, r_k, out))
     gs = _gs32(graph_scale) if H_G else None
     lse = lse.contiguous()
     delta = torch.empty(B, H, S, device=q.device, dtype=torch.float32)
     dq, dk, dv, dr_q, dr_k = _grads_like(q, k, v, r_q, r_k, H_G)
     d_gs = torch.empty(max(H_G, 1), device=q.device, dtype=torch.float32)
-    prob = _problem(False, B, S, S_k, 0, 0, H, H_KV, H_G, D, R, is_causal, softmax_scale)
+    prob = _problem(False, B, S, S_k, 0, 0, H, H_KV, H_G, D, R, is_causal, softmax_scale,
+                    dtype=q.dtype)
     _run_bwd(prob, (dout, q, k, v, r_q if H_G else None, r_k if H_G else None, gs, out, lse,
                     delta, dq, dk, dv, dr_q, dr_k, d_gs if H_G else None), _view4)
     return dq, dk, dv, dr_q, dr_k, _dgs_out(d_gs, H_G, graph_scale)
@@ -365,7 +383,7 @@ def _fna2_backward_varlen(
     H_G = 0 if r_q is None else r_q.shape[1]
     R = 0 if r_q is None else r_q.shape[2]
     N = cu_seqlens_q.shape[0] - 1
-    dout = _prep(dout)
+    dout = _prep(dout if dout.dtype == q.dtype else dout.to(q.dtype))  # as do.to(v.dtype), :522
     q, k, v, r_q, r_k, out = (_prep(t) for t in (q, k, v, r_q, r_k, out))
     cu_q = cu_seqlens_q.to(device=q.device, dtype=torch.int32).contiguous()
     cu_k = cu_seqlens_k.to(device=q.device, dtype=torch.int32).contiguous()
@@ -377,7 +395,7 @@ def _fna2_backward_varlen(
     dq, dk, dv, dr_q, dr_k = _grads_like(q, k, v, r_q, r_k, H_G)
     d_gs = torch.empty(max(H_G, 1), device=q.device, dtype=torch.float32)
     prob = _problem(True, N, max_seqlen_q, max_seqlen_k, total_q, total_k, H, H_KV, H_G, D, R,
-                    is_causal, softmax_scale, cu_q, cu_k)
+                    is_causal, softmax_scale, cu_q, cu_k, dtype=q.dtype)
     _run_bwd(prob, (dout, q, k, v, r_q if H_G else None, r_k if H_G else None, gs, out, lse,
                     delta, dq, dk, dv, dr_q, dr_k, d_gs if H_G else None), _view3, plan)
     return dq, dk, dv, dr_q, dr_k, _dgs_out(d_gs, H_G, graph_scale)
@@ -388,7 +406,7 @@ def _plan_for(q, k, r_q, cu_q, cu_k, max_q, max_k, is_causal, scale):
     H_G = 0 if r_q is None else r_q.shape[1]
     R = 0 if r_q is None else r_q.shape[2]
     prob = _problem(True, cu_q.shape[0] - 1, max_q, max_k, q.shape[0], k.shape[0], q.shape[1],
-                    k.shape[1], H_G, q.shape[2], R, is_causal, scale, cu_q, cu_k)
+                    k.shape[1], H_G, q.shape[2], R, is_causal, scale, cu_q, cu_k, dtype=q.dtype)
     return new_plan(prob, q.device)
 
 
@@ -427,7 +445,7 @@ class FlashNaylisAttnFunc(torch.autograd.Function):
             out, lse = _fna2_forward_varlen(
                 q, k, v, r_q, r_k, graph_scale,
                 cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
-                softmax_scale, is_causal, plan=plan,
+                softmax_scale, is_causal, plan=plan, lse_head_major=True,
             )
             ctx.plan = plan
         else:

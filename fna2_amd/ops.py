@@ -87,7 +87,7 @@ def fna2_fwd(q: Tensor, k: Tensor, v: Tensor, r_q: Optional[Tensor], r_k: Option
                          softmax_scale)
         out, lse = _fna2_forward_varlen(q, k, v, r_q, r_k, graph_scale, cu_seqlens_q, cu_k,
                                         max_seqlen_q, max_seqlen_k, softmax_scale, is_causal,
-                                        plan=plan)
+                                        plan=plan, lse_head_major=True)
         if plan is None:
             plan = q.new_empty((0,), dtype=torch.uint8)
     return _like(q, out), lse, plan

@@ -40,8 +40,12 @@ extern "C" {
 
 #define FNA2_ABI_VERSION 2
 
-/* Element types.  The attention entry points take FNA2_BF16 (q, k, v, r_q,
- * r_k, out, dout and the gradients); fna2_rope_varlen takes all three. */
+/* Element types.  The attention entry points (fna2_fwd, fna2_bwd,
+ * fna2_fwd_noalloc) take FNA2_BF16 or FNA2_F16 for q, k, v, out, dout, dq,
+ * dk and dv; r_q, r_k, dr_q and dr_k are bf16 either way (the reference
+ * asserts bf16 ranks, FNA2/flash_naylis_attn.py:1419-1420, and is generic
+ * over the q/k/v dtype, :187, :201, :522-529).  fna2_rope_varlen takes all
+ * three; fna2_decode takes bf16. */
 enum fna2_dtype { FNA2_BF16 = 1, FNA2_F16 = 2, FNA2_F32 = 3 };
 
 /* Return codes. */

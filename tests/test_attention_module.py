@@ -448,3 +448,62 @@ def test_stacked_projection_gradient_paths_agree():
         torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)
     torch.testing.assert_close(g1[0], g_all @ w_all, rtol=1e-5, atol=1e-5)
     torch.testing.assert_close(torch.cat(g1[1:]), g_all.t() @ x.detach(), rtol=1e-5, atol=1e-5)
+
+
+def test_stacked_projection_under_autocast_with_fp32_params():
+    """Mixed precision: fp32 parameters under autocast(bf16).  The one-GEMM
+    projection runs in bf16 as F.linear does; its backward returns dx in x's
+    dtype and dW in the weights' dtype, equal to five autocast nn.Linear
+    projections' gradients."""
+    torch.manual_seed(12)
+    m = A.NaylisAttention(64, 4, n_kv_heads=2, rel_rank=8)
+    ref = copy.deepcopy(m)
+    x = torch.randn(2, 6, 64)
+    sizes = [64, 32, 32, 32, 32]
+    cot = [torch.randn(12, n) for n in sizes]
+    x1 = x.clone().requires_grad_(True)
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        outs = A._StackedProjection.apply(x1, m._pack_projection_weights(), sizes,
+                                          *m._projection_weights())
+    assert all(o.dtype == torch.bfloat16 for o in outs)
+    loss1 = sum((o.reshape(12, -1).float() * c).sum() for o, c in zip(outs, cot))
+    g1 = torch.autograd.grad(loss1, [x1, *m._projection_weights()])
+    assert g1[0].dtype == torch.float32 and all(g.dtype == torch.float32 for g in g1[1:])
+
+    x2 = x.clone().requires_grad_(True)
+    mods = [ref.q_proj, ref.k_proj, ref.v_proj, ref.rel_q_proj, ref.rel_k_proj]
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        sep = [mod(x2) for mod in mods]
+    loss2 = sum((o.reshape(12, -1).float() * c).sum() for o, c in zip(sep, cot))
+    g2 = torch.autograd.grad(loss2, [x2, *ref._projection_weights()])
+    for a, b in zip(g1, g2):
+        torch.testing.assert_close(a, b, rtol=2e-2, atol=2e-2)
+
+    # the module's forward + backward under autocast with fp32 params
+    m2 = copy.deepcopy(ref)
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        y = m2(x.clone().requires_grad_(True))[0]
+    y.float().sum().backward()
+    assert all(p.grad is not None and p.grad.dtype == torch.float32
+               for p in m2._projection_weights())
+
+
+def test_stacked_projection_frozen_and_unused_weights():
+    """As for nn.Linear: a frozen weight gets no gradient (no dW GEMM), and a
+    block whose output does not reach the loss gets None, not zeros."""
+    torch.manual_seed(13)
+    m = A.NaylisAttention(64, 4, n_kv_heads=2, rel_rank=8)
+    ws = m._projection_weights()
+    ws[1].requires_grad_(False)  # k_proj frozen
+    sizes = [64, 32, 32, 32, 32]
+    x = torch.randn(5, 64, requires_grad=True)
+    outs = A._StackedProjection.apply(x, m._pack_projection_weights(), sizes, *ws)
+    loss = outs[0].sum() + outs[1].sum() + outs[2].sum() + outs[3].sum()  # rel_k unused
+    loss.backward()
+    assert ws[1].grad is None
+    assert ws[4].grad is None
+    for i in (0, 2, 3):
+        torch.testing.assert_close(ws[i].grad, torch.ones(5, sizes[i]).t() @ x.detach(),
+                                   rtol=1e-5, atol=1e-5)
+    w_all = m._pack_projection_weights()
+    torch.testing.assert_close(x.grad, torch.ones(5, 160) @ w_all[:160], rtol=1e-5, atol=1e-5)

@@ -121,8 +121,14 @@ def test_check_fwd_accepts_valid_dense(lib):
     assert check_fwd(lib, _fwd()) == "FNA2_OK"
 
 
+def test_check_fwd_accepts_fp16(lib):
+    # fp16 q/k/v (FNA2_F16), as the reference's kernels are generic over it
+    assert check_fwd(lib, _fwd(dtype=_capi.FNA2_F16)) == "FNA2_OK"
+
+
 @pytest.mark.parametrize("over,code", [
-    (dict(dtype=2), "FNA2_E_DTYPE"),
+    (dict(dtype=3), "FNA2_E_DTYPE"),
+    (dict(dtype=0), "FNA2_E_DTYPE"),
     (dict(head_dim=96), "FNA2_E_HEAD_DIM"),
     (dict(rank=12), "FNA2_E_RANK"),
     (dict(rank=72), "FNA2_E_RANK"),

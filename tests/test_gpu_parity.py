@@ -361,6 +361,58 @@ def test_backward_ignores_a_plan_no_forward_filled(gpu):
     H.check_grads(grads, ref_g)
 
 
+def test_plan_of_another_key_tile_size_is_ignored(gpu):
+    """A plan filled by a d = 128 forward (128-key dK/dV tiles) handed to a
+    d = 64, rank-16 backward of the same sequences (256-key tiles): the key
+    list's records differ, so the backward must not use it.  Its gradients
+    equal those of the same backward without a plan, bit for bit."""
+    F = _fna2()
+    lengths = [300, 65, 513, 1]
+    cu = torch.tensor([0] + list(np.cumsum(lengths)), dtype=torch.int32, device=gpu)
+    big = H.make_varlen(lengths, 2, 128, 2, 2, 32, seed=5)
+    gb = [t.to(gpu) for t in big]
+    plan = F._plan_for(gb[0], gb[1], gb[3], cu, cu, 513, 513, True, 0.1)
+    F._fna2_forward_varlen(*gb[:6], cu, cu, 513, 513, 0.1, True, plan=plan)
+    (q, k, v, rq, rk, gs_, dout, cu_q, cu_k) = H.make_varlen(lengths, 4, 64, 2, 4, 16, seed=6)
+    g = [t.to(gpu) for t in (q, k, v, rq, rk, gs_, dout)]
+    small = F._plan_for(g[0], g[1], g[3], cu, cu, 513, 513, True, 0.125)
+    assert plan.numel() >= small.numel()
+    out, lse = F._fna2_forward_varlen(*g[:6], cu, cu, 513, 513, 0.125, True)
+    print("d64 r16 backward with a d128 plan", flush=True)
+    with_plan = F._fna2_backward_varlen(g[6], *g[:6], out, lse, cu, cu, 513, 513, 0.125, True,
+                                        plan=plan)
+    no_plan = F._fna2_backward_varlen(g[6], *g[:6], out, lse, cu, cu, 513, 513, 0.125, True)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("dq", "dk", "dv", "drq", "drk", "dgs"), with_plan, no_plan):
+        assert torch.equal(a, b), name
+    ref_out, ref_lse, ref_g = H.oracle_fwd_bwd(q, k, v, rq, rk, gs_, dout, 0.125, True,
+                                               cu_q.numpy(), cu_k.numpy())
+    H.check_grads(with_plan, ref_g)
+
+
+def test_varlen_lse_layout_matches_reference(gpu):
+    """_fna2_forward_varlen returns lse as a contiguous [T, H] tensor, as the
+    reference allocates it (flash_naylis_attn.py:780), with the same values
+    as the head-major view the autograd path keeps; the backward reads
+    either."""
+    F = _fna2()
+    lengths = [129, 7, 256]
+    (q, k, v, rq, rk, gs_, dout, cu_q, cu_k) = H.make_varlen(lengths, 4, 128, 2, 4, 32, seed=8)
+    g = [t.to(gpu) for t in (q, k, v, rq, rk, gs_, dout, cu_q, cu_k)]
+    out, lse = F._fna2_forward_varlen(*g[:6], g[7], g[8], 256, 256, 0.09, True)
+    out2, lse_hm = F._fna2_forward_varlen(*g[:6], g[7], g[8], 256, 256, 0.09, True,
+                                          lse_head_major=True)
+    assert lse.shape == (sum(lengths), 4) and lse.is_contiguous()
+    assert lse_hm.shape == lse.shape and lse_hm.stride() == (1, sum(lengths))
+    assert torch.equal(lse, lse_hm) and torch.equal(out, out2)
+    lse.view(-1)  # flat views work, as on the reference's tensor
+    ga = F._fna2_backward_varlen(g[6], *g[:6], out, lse, g[7], g[8], 256, 256, 0.09, True)
+    gb = F._fna2_backward_varlen(g[6], *g[:6], out, lse_hm, g[7], g[8], 256, 256, 0.09, True)
+    torch.cuda.synchronize()
+    for a, b in zip(ga, gb):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("mode", ["varlen", "dense"])
 def test_rank_features_past_r_are_never_read(gpu, mode):
     """R = 16 with R_q / R_k as views into 32-wide rows whose other 16
