@@ -54,7 +54,9 @@ namespace {
 
 enum : unsigned { kTileQ = 1, kTileR = 2, kTileO = 4, kTileL = 8, kTileAll = 15 };
 
-template <int D, int RPL, bool F16>
+// RS: 16-deep rank steps of the score chain (RPL / 16, or 1 where R <= 16:
+// the second step of a 32-wide rank tile would multiply zeros).
+template <int D, int RPL, bool F16, int RS>
 struct KvCfg {
   static constexpr int NP = 4;       // producer waves (as many consumers)
   static constexpr int NW = 2 * NP;  // waves per workgroup
@@ -65,7 +67,8 @@ struct KvCfg {
   static constexpr int CD = D / 8;
   static constexpr int CR = RPL > 0 ? RPL / 8 : 4;
   static constexpr int KSD = D / 16;
-  static constexpr int KSR = RPL / 16;
+  static constexpr int KSR = RS;
+  static_assert(RS * 16 <= RPL && (RPL == 0) == (RS == 0), "rank steps within the rank tile");
   static constexpr int NDB = D / 32;
   static constexpr int NRB = RPL / 32;
   static constexpr int QB = BM * D * 2;
@@ -220,9 +223,9 @@ struct RingDma {
   }
 };
 
-template <int D, int RPL, bool F16>
+template <int D, int RPL, bool F16, int RS>
 __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
-  using C = KvCfg<D, RPL, F16>;
+  using C = KvCfg<D, RPL, F16, RS>;
   __shared__ __attribute__((aligned(1024))) uint8_t st0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t st1[C::STAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t st2[C::STAGE];
@@ -946,22 +949,25 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
   }
 }
 
-// One non-template kernel per (D, padded rank, element type) so that each
-// has a host stub.
-#define FNA2_DKDV_KERNEL(D, RPL)                                                       \
-  __global__ __launch_bounds__(512, 1) void dkdv_kernel_d##D##_r##RPL(const BwdParams P) { \
-    dkdv_body<D, RPL, false>(P);                                                       \
-  }                                                                                    \
-  __global__ __launch_bounds__(512, 1) void dkdv_kernel_d##D##_r##RPL##_f16(             \
-      const BwdParams P) {                                                             \
-    dkdv_body<D, RPL, true>(P);                                                        \
+// One non-template kernel per (D, rank, element type) so that each has a
+// host stub.  Rank names: 0, 32 and 64 are the padded rank tiles; 16 is the
+// 32-wide tile with one rank step (R <= 16).
+#define FNA2_DKDV_KERNEL(D, RNAME, RPL, RS)                                              \
+  __global__ __launch_bounds__(512, 1) void dkdv_kernel_d##D##_r##RNAME(const BwdParams P) { \
+    dkdv_body<D, RPL, false, RS>(P);                                                     \
+  }                                                                                      \
+  __global__ __launch_bounds__(512, 1) void dkdv_kernel_d##D##_r##RNAME##_f16(             \
+      const BwdParams P) {                                                               \
+    dkdv_body<D, RPL, true, RS>(P);                                                      \
   }
-FNA2_DKDV_KERNEL(64, 0)
-FNA2_DKDV_KERNEL(64, 32)
-FNA2_DKDV_KERNEL(64, 64)
-FNA2_DKDV_KERNEL(128, 0)
-FNA2_DKDV_KERNEL(128, 32)
-FNA2_DKDV_KERNEL(128, 64)
+FNA2_DKDV_KERNEL(64, 0, 0, 0)
+FNA2_DKDV_KERNEL(64, 16, 32, 1)
+FNA2_DKDV_KERNEL(64, 32, 32, 2)
+FNA2_DKDV_KERNEL(64, 64, 64, 4)
+FNA2_DKDV_KERNEL(128, 0, 0, 0)
+FNA2_DKDV_KERNEL(128, 16, 32, 1)
+FNA2_DKDV_KERNEL(128, 32, 32, 2)
+FNA2_DKDV_KERNEL(128, 64, 64, 4)
 #undef FNA2_DKDV_KERNEL
 
 }  // namespace
@@ -969,18 +975,23 @@ FNA2_DKDV_KERNEL(128, 64)
 hipError_t launch_bwd_dkdv(const BwdParams& P, int rpl, int grid, hipStream_t s) {
   if (grid <= 0) return hipSuccess;
   void (*k)(const BwdParams) = nullptr;
+  const bool r16 = rpl == 32 && P.p.R <= 16;  // one rank step
   if (P.p.f16) {
     if (P.p.D == 64)
       k = rpl == 0 ? dkdv_kernel_d64_r0_f16
-                   : rpl == 32 ? dkdv_kernel_d64_r32_f16 : dkdv_kernel_d64_r64_f16;
+          : rpl == 32 ? (r16 ? dkdv_kernel_d64_r16_f16 : dkdv_kernel_d64_r32_f16)
+                      : dkdv_kernel_d64_r64_f16;
     if (P.p.D == 128)
       k = rpl == 0 ? dkdv_kernel_d128_r0_f16
-                   : rpl == 32 ? dkdv_kernel_d128_r32_f16 : dkdv_kernel_d128_r64_f16;
+          : rpl == 32 ? (r16 ? dkdv_kernel_d128_r16_f16 : dkdv_kernel_d128_r32_f16)
+                      : dkdv_kernel_d128_r64_f16;
   } else {
     if (P.p.D == 64)
-      k = rpl == 0 ? dkdv_kernel_d64_r0 : rpl == 32 ? dkdv_kernel_d64_r32 : dkdv_kernel_d64_r64;
+      k = rpl == 0 ? dkdv_kernel_d64_r0
+          : rpl == 32 ? (r16 ? dkdv_kernel_d64_r16 : dkdv_kernel_d64_r32) : dkdv_kernel_d64_r64;
     if (P.p.D == 128)
-      k = rpl == 0 ? dkdv_kernel_d128_r0 : rpl == 32 ? dkdv_kernel_d128_r32 : dkdv_kernel_d128_r64;
+      k = rpl == 0 ? dkdv_kernel_d128_r0
+          : rpl == 32 ? (r16 ? dkdv_kernel_d128_r16 : dkdv_kernel_d128_r32) : dkdv_kernel_d128_r64;
   }
   if (!k || (rpl != 0 && rpl != 32 && rpl != 64)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k, dim3(grid), dim3(512), 0, s, P);
