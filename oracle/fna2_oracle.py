@@ -138,6 +138,36 @@ def head_backward(dO, Q, K, V, Rq, Rk, g, scale, causal, O, lse):
     return dQ, dK, dV, dRq, dRk, dg
 
 
+def head_rows(dO, Q, K, V, Rq, Rk, g, scale, causal, rows, eps=EPS):
+    """The row-local results of one (sequence, head) for the query rows
+    ``rows`` only: (out, lse, dQ, dRq) of those rows, each of which needs every
+    key but no other query row -- the same formulas as ``head_forward`` and
+    ``head_backward`` (delta from these rows' own output), for checking long
+    sequences on a row subset.  (dK, dV, dRk and dg sum over every query row
+    and are not row-local.)"""
+    i = np.asarray(rows, dtype=np.int64)
+    lk = K.shape[0]
+    Rqi = None if Rq is None else Rq[i]
+    S = _scores(Q[i], K, Rqi, Rk, g, scale)
+    vis = np.ones((len(i), lk), dtype=bool)
+    if causal:
+        vis &= np.arange(lk)[None, :] <= i[:, None]
+    S = np.where(vis, S, -np.inf)
+    m = S.max(axis=1) if lk else np.full(len(i), -np.inf)
+    live = np.isfinite(m)
+    msafe = np.where(live, m, 0.0)
+    P = np.where(vis, np.exp(S - msafe[:, None]), 0.0)
+    l = P.sum(axis=1)
+    O = (P @ V) / (l + eps)[:, None]
+    lse = np.where(live, m + np.log(l + eps), -np.inf)
+    Pn = np.where(vis & live[:, None], np.exp(np.where(vis, S, 0.0) - np.where(live, lse, 0.0)[:, None]), 0.0)
+    delta = (dO[i] * O).sum(axis=1)
+    dS = Pn * (dO[i] @ V.T - delta[:, None])
+    dQ = scale * (dS @ K)
+    dRq = None if Rq is None else g * (dS @ Rk)
+    return O, lse, dQ, dRq
+
+
 def _segments(varlen, n, cu_q, cu_k, Sq, Sk):
     if varlen:
         cq = np.asarray(cu_q, dtype=np.int64)

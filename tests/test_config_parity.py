@@ -12,15 +12,25 @@ oracle on the same bf16 inputs:
 
 c4 (B1 H32 L16384 d128 r64) runs all 32 heads on the GPU; its heads are
 independent (H_KV = H_G = H), so the oracle checks a full-length subset of
-them (heads 0 and 31, every one of the 16,384 rows) exactly.  c1 is the
-CPU-only fp32 case (tests/test_oracle.py::test_c1_fp32_within_1e4_of_fp64).
+them (heads 0 and 31, every one of the 16,384 rows) exactly, and every head
+on a row subset: out, LSE, dQ and dR_q of the first and the last 256 rows
+(row-local results, ``oracle.head_rows``; the last rows see all 16,384
+keys).  c1 is the CPU-only fp32 case
+(tests/test_oracle.py::test_c1_fp32_within_1e4_of_fp64).
+
+With ``FNA2_PARITY_OUT`` set to a directory, each test also writes its
+measured errors there (``parity_<config>.json``): the margins under the
+bounds, as the reference's own check prints its diffs
+(validate_fna2.py:115-122).
 
 The reference validates at its own shapes in validate_fna2.py:129-173
 (configs :44-57); ``large_seq`` is B1 H8 S512 D64 H_KV4 H_G4 R32 with R
 drawn at std 1 (:67-81).
 """
 import importlib
+import json
 import math
+import os
 
 import numpy as np
 import pytest
@@ -59,12 +69,34 @@ def _run_gpu(inp, causal, gpu):
     return out.detach(), lse, [g.detach() for g in grads]
 
 
-def _check_config(name, gpu, heads=None):
+def _record(name, **errs):
+    """Writes the measured errors of a config to $FNA2_PARITY_OUT (if set)."""
+    d = os.environ.get("FNA2_PARITY_OUT")
+    if not d:
+        return
+    os.makedirs(d, exist_ok=True)
+    rec = {"config": name, "bounds": {"out_max_abs": H.TOL_OUT, "lse_max_abs": H.TOL_LSE,
+                                      "grad_rel_norm": H.TOL_GRAD}}
+    rec.update({k: (round(float(v), 6) if isinstance(v, (float, np.floating)) else v)
+                for k, v in errs.items()})
+    with open(os.path.join(d, f"parity_{name}.json"), "w") as f:
+        json.dump(rec, f, indent=1)
+
+
+def _lse_err(lse, ref_lse):
+    l = lse.detach().double().cpu().numpy()
+    r = np.asarray(ref_lse, np.float64)
+    fin = np.isfinite(r)
+    return float(np.max(np.abs(l[fin] - r[fin]))) if fin.any() else 0.0
+
+
+def _check_config(name, gpu, heads=None, keep=None):
     cfg = configs.get(name)
     inp = configs.make_inputs(cfg)
     print(f"config {name}: {cfg.desc}; tokens {cfg.total}, seqs {len(cfg.seq_lengths())}",
           flush=True)
     out, lse, grads = _run_gpu(inp, cfg.causal, gpu)
+    full = (inp, out, lse, grads)
     cu = None if inp.cu_seqlens is None else inp.cu_seqlens.numpy()
     args = [inp.q, inp.k, inp.v, inp.r_q, inp.r_k, inp.graph_scale, inp.dout]
     if heads is not None:  # dense [B, H, S, *] views: a head subset, every row
@@ -79,6 +111,15 @@ def _check_config(name, gpu, heads=None):
     errs = H.check_grads(grads, ref_g)
     print(f"config {name}: out max abs {e_out:.2e}; grad rel-norm "
           + ", ".join(f"{k} {v:.2e}" for k, v in errs.items()), flush=True)
+    rec = dict(out_max_abs=e_out, lse_max_abs=_lse_err(lse, ref_lse),
+               grad_rel_norm={k: round(float(v), 6) for k, v in errs.items()})
+    if heads is not None:
+        rec["heads_checked_full"] = heads
+    if keep is not None:
+        keep.update(rec)
+    else:
+        _record(name, **rec)
+    return full
 
 
 def test_config_c2_dense_causal(gpu):
@@ -89,8 +130,43 @@ def test_config_c3_varlen_causal(gpu):
     _check_config("c3", gpu)
 
 
-def test_config_c4_long_context_heads_0_and_31(gpu):
-    _check_config("c4", gpu, heads=[0, 31])
+def test_config_c4_long_context(gpu):
+    """Heads 0 and 31 in full (every row, all six gradients), then all 32
+    heads on the first and last 256 rows (out, LSE, dQ, dR_q)."""
+    from oracle import fna2_oracle as oracle
+
+    cfg = configs.get("c4")
+    rec = {}
+    inp, out, lse, grads = _check_config("c4", gpu, heads=[0, 31], keep=rec)
+    L, nh = cfg.L, cfg.H
+    rows = list(range(256)) + list(range(L - 256, L))
+    f64 = lambda t: t.detach().double().cpu().numpy()
+    worst_out, worst_lse = 0.0, 0.0
+    num = {"dq": 0.0, "drq": 0.0}
+    den = {"dq": 0.0, "drq": 0.0}
+    for h in range(nh):
+        o, l, dq, drq = oracle.head_rows(
+            f64(inp.dout[0, h]), f64(inp.q[0, h]), f64(inp.k[0, h]), f64(inp.v[0, h]),
+            f64(inp.r_q[0, h]), f64(inp.r_k[0, h]), float(inp.graph_scale[h]), inp.scale,
+            cfg.causal, rows)
+        worst_out = max(worst_out, H.max_abs(out[0, h, rows], o))
+        worst_lse = max(worst_lse, _lse_err(lse[0, h, rows], l))
+        for name, got, ref in (("dq", grads[0][0, h, rows], dq), ("drq", grads[3][0, h, rows], drq)):
+            g = f64(got)
+            num[name] += float(np.sum((g - ref) ** 2))
+            den[name] += float(np.sum(ref ** 2))
+    rel = {k: math.sqrt(num[k]) / max(math.sqrt(den[k]), 1e-12) for k in num}
+    print(f"config c4, all {nh} heads, rows [0, 256) and [{L - 256}, {L}): out max abs "
+          f"{worst_out:.2e}, lse {worst_lse:.2e}, dq {rel['dq']:.2e}, drq {rel['drq']:.2e}",
+          flush=True)
+    assert worst_out < H.TOL_OUT and worst_lse < H.TOL_LSE
+    assert rel["dq"] < H.TOL_GRAD and rel["drq"] < H.TOL_GRAD
+    rec["all_heads_row_subset"] = {"rows": "[0, 256) and [16128, 16384) of every head",
+                                   "out_max_abs": round(worst_out, 6),
+                                   "lse_max_abs": round(worst_lse, 6),
+                                   "dq_rel_norm": round(rel["dq"], 6),
+                                   "drq_rel_norm": round(rel["drq"], 6)}
+    _record("c4", **rec)
 
 
 def test_config_c5_skewed_varlen_noncausal(gpu):
@@ -109,5 +185,7 @@ def test_reference_large_seq_config(gpu):
     _, lse = F._fna2_forward(*[t.detach() for t in leaves], scale, True)
     torch.cuda.synchronize()
     ref_out, ref_lse, ref_g = H.oracle_fwd_bwd(q, k, v, rq, rk, gs, dout, scale, True)
-    H.check_out(out, lse, ref_out, ref_lse)
-    H.check_grads(grads, ref_g)
+    e_out = H.check_out(out, lse, ref_out, ref_lse)
+    errs = H.check_grads(grads, ref_g)
+    _record("large_seq", out_max_abs=e_out, lse_max_abs=_lse_err(lse, ref_lse),
+            grad_rel_norm={k: round(float(v), 6) for k, v in errs.items()})

@@ -172,6 +172,27 @@ def test_identities():
         assert abs(x - y) < 1e-9 * max(1, abs(x)) and abs(x - z) < 1e-9 * max(1, abs(x))
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_head_rows_equals_the_full_head_on_its_rows(causal):
+    """head_rows (row-local out, lse, dQ, dRq of a row subset) against the
+    pinned head_forward / head_backward on the same rows; also across
+    head_forward's 1024-row chunk boundary, and for a vanilla head."""
+    rng = np.random.default_rng(21)
+    L, D, R = 1100, 8, 4
+    Q, K, V, dO = (rng.standard_normal((L, D)) for _ in range(4))
+    Rq, Rk = rng.standard_normal((L, R)) * 0.5, rng.standard_normal((L, R)) * 0.5
+    rows = [0, 1, 5, 1023, 1024, 1050, L - 1]
+    for g, rq, rk in ((0.7, Rq, Rk), (0.0, None, None)):
+        o, l = O.head_forward(Q, K, V, rq, rk, g, 0.3, causal)
+        dq, _, _, drq, _, _ = O.head_backward(dO, Q, K, V, rq, rk, g, 0.3, causal, o, l)
+        o2, l2, dq2, drq2 = O.head_rows(dO, Q, K, V, rq, rk, g, 0.3, causal, rows)
+        np.testing.assert_allclose(o2, o[rows], atol=1e-12)
+        np.testing.assert_allclose(l2, l[rows], atol=1e-12)
+        np.testing.assert_allclose(dq2, dq[rows], atol=1e-11)
+        if rq is not None:
+            np.testing.assert_allclose(drq2, drq[rows], atol=1e-11)
+
+
 def test_noncausal_key_permutation_invariance():
     q, k, v, rq, rk, gs, _ = make(B=1, H=2, S=9, D=5, HKV=2, HG=2, R=3, seed=10)
     o, _ = O.forward(q, k, v, rq, rk, gs, 0.5, False)
