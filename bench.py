@@ -12,9 +12,12 @@ algorithmic FLOPs: 4d+2r forward and 10d+6r backward per visible
 (query, key) pair per head), the forward-only throughput, fractions of the
 bf16 dense MFMA peak, a ``roofline`` object for the kernel that takes the
 most time per step (per-launch durations from HIP events that the library
-records on its launch stream, in a second pass of the same steps: event
+records on its launch stream, in a separate pass of the same steps: event
 records between dependent kernels add a few microseconds each, so the timed
-steps run without them), and a ``cpu_baseline``
+steps run without them), the durations of the warmup steps and of the
+kernels in a first per-kernel pass (the device's clock ramp after the idle
+start: that pass and the forward-only one run before the W warmup and K
+timed steps), and a ``cpu_baseline``
 object: the reference's eager path (SDPA + materialised bias, restated in
 ``oracle/eager_reference.py``) timed on this host's cores on a bounded
 sample of the same workload.
@@ -822,29 +825,37 @@ def main():
         out = fwd()
         torch.autograd.grad(out, leaves, inp.dout)
 
+    # Passes, in this order (the device idles while the process starts, and
+    # its clocks come up only over the first few dozen steps):
+    #  1. W warmup steps, each bracketed by events ("warmup_step_ms");
+    #  2. K steps with HIP events around every kernel ("first_pass_kernel_us":
+    #     the kernels during that ramp);
+    #  3. the forward alone: W warmup + K timed forwards;
+    #  4. W warmup + K timed fwd+bwd steps: `value`;
+    #  5. K steps with HIP events around every kernel again: the per-kernel
+    #     durations of the roofline, on a device at its working clocks (event
+    #     records between dependent kernels add a few microseconds each, so
+    #     the timed steps run without them).
+    def kernel_pass():
+        timer = F.KernelTimer(args.steps, args.steps)
+        torch.cuda.synchronize()
+        with F.kernel_timing(timer):
+            for _ in range(args.steps):
+                step()
+        torch.cuda.synchronize()
+        return {k: statistics.mean(v) for k, v in timer.durations_ms().items()}
+
+    ramp = []
     for _ in range(args.warmup):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
         step()
-    torch.cuda.synchronize()
+        b.record()
+        torch.cuda.synchronize()
+        ramp.append(round(a.elapsed_time(b), 4))
+    kdur_first = kernel_pass()
 
-    # fwd+bwd, timed on the current stream
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(args.steps):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    ms_step = e0.elapsed_time(e1) / args.steps
-
-    # per-kernel durations: the same steps again, with events around kernels
-    timer = F.KernelTimer(args.steps, args.steps)
-    torch.cuda.synchronize()
-    with F.kernel_timing(timer):
-        for _ in range(args.steps):
-            step()
-    torch.cuda.synchronize()
-    kdur = {k: statistics.mean(v) for k, v in timer.durations_ms().items()}
-
     # forward only
     with torch.no_grad():
         for _ in range(args.warmup):
@@ -856,6 +867,19 @@ def main():
         e1.record()
         torch.cuda.synchronize()
     ms_fwd = e0.elapsed_time(e1) / args.steps
+
+    # fwd+bwd, timed on the current stream
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_step = e0.elapsed_time(e1) / args.steps
+
+    kdur = kernel_pass()
 
     # cache-flushed step (256 MB MALL): 512 MB written between timed steps
     ms_flushed = None
@@ -933,6 +957,8 @@ def main():
         "tflops_flushed": None if ms_flushed is None else
         round((fwd_flops + bwd_flops) / (ms_flushed * 1e-3) / 1e12, 2),
         "kernel_us": {k: round(v * 1e3, 2) for k, v in kdur.items()},
+        "warmup_step_ms": ramp,
+        "first_pass_kernel_us": {k: round(v * 1e3, 2) for k, v in kdur_first.items()},
         "roofline": roof,
     }
     if not args.no_cpu:
