@@ -88,6 +88,7 @@ class FwdArgs(ctypes.Structure):
         ("events", ctypes.c_void_p),
         ("plan", ctypes.c_void_p),
         ("plan_bytes", ctypes.c_size_t),
+        ("plan_filled", ctypes.c_int32),
     ]
 
 

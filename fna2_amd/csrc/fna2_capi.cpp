@@ -447,17 +447,21 @@ int fwd_launch(const fna2_fwd_args* a, void* ws, hipStream_t stream) {
   K.gs = a->graph_scale;
   const Grids g = grids(p);
   if (p.varlen && use_plan(a->plan, p)) {
-    // One launch builds this call's list and the backward's key-tile list.
+    // One launch builds this call's list and the backward's key-tile list,
+    // unless the caller vouches that an earlier forward of this problem
+    // filled the plan (and our record of it agrees).
     const PlanLayout L = plan_layout(p);
     char* pl = (char*)a->plan;
     fna2::TileRec* tiles = (fna2::TileRec*)(pl + L.tiles_q);
     int* count = (int*)(pl + L.count_q);
-    const fna2::TileList lq{{0, kFwdBM, kFwdBN, 1}, tiles, count, (int)g.fwd_bound};
-    const fna2::TileList lk{{1, kv_tile(p), kKvBM, 0}, (fna2::TileRec*)(pl + L.tiles_k),
-                            (int*)(pl + L.count_k), (int)g.kv_bound};
-    if (fna2::launch_build_tiles(K.p, lq, &lk, nullptr, stream) != hipSuccess)
-      return FNA2_E_LAUNCH;
-    plan_register(a->plan, p);
+    if (!(a->plan_filled && plan_filled_for(a->plan, p))) {
+      const fna2::TileList lq{{0, kFwdBM, kFwdBN, 1}, tiles, count, (int)g.fwd_bound};
+      const fna2::TileList lk{{1, kv_tile(p), kKvBM, 0}, (fna2::TileRec*)(pl + L.tiles_k),
+                              (int*)(pl + L.count_k), (int)g.kv_bound};
+      if (fna2::launch_build_tiles(K.p, lq, &lk, nullptr, stream) != hipSuccess)
+        return FNA2_E_LAUNCH;
+      plan_register(a->plan, p);
+    }
     if (rows_q(p) == 0) return FNA2_OK;
     K.tiles = tiles;
     K.n_tiles = count;

@@ -35,6 +35,7 @@ reference.
 """
 from __future__ import annotations
 
+import collections
 import contextlib
 import ctypes
 import math
@@ -208,7 +209,7 @@ def new_plan(prob: _capi.Problem, device) -> Optional[torch.Tensor]:
     return torch.empty(n, dtype=torch.uint8, device=device) if n > 0 else None
 
 
-def _run_fwd(prob, q, k, v, r_q, r_k, gs, out, lse, view, plan=None):
+def _run_fwd(prob, q, k, v, r_q, r_k, gs, out, lse, view, plan=None, plan_filled=False):
     L = _capi.lib()
     ws = _workspace(L.fna2_fwd_workspace_bytes, prob, q.device)
     ev = _events(KernelTimer.FWD)
@@ -217,6 +218,7 @@ def _run_fwd(prob, q, k, v, r_q, r_k, gs, out, lse, view, plan=None):
                          ctypes.cast(ev, ctypes.c_void_p) if ev is not None else None)
     if plan is not None:
         args.plan, args.plan_bytes = plan.data_ptr(), plan.numel()
+        args.plan_filled = int(bool(plan_filled))
     with torch.cuda.device(q.device):
         st = L.fna2_fwd(ctypes.byref(args), _stream(q.device))
     _capi.raise_for(st, "fna2_fwd")
@@ -289,6 +291,7 @@ def _fna2_forward_varlen(
     is_causal: bool = True,
     plan: Optional[torch.Tensor] = None,
     lse_head_major: bool = False,
+    plan_filled: bool = False,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Varlen forward; returns (out [T,H,D], lse [T,H]).  Mirrors :756-804.
     ``plan`` (from ``new_plan``, optional): also build the backward's tile
@@ -299,7 +302,10 @@ def _fna2_forward_varlen(
     returns the same values as a ``[T, H]`` view of head-major ``[H, T]``
     memory instead: a forward workgroup's 128 rows of one head are then one
     contiguous run (row-major ``[T, H]`` puts each 4-byte value in its own
-    64-byte segment: 75.9 MB written per c3 forward against 68.2)."""
+    64-byte segment: 75.9 MB written per c3 forward against 68.2).
+    ``plan_filled``: an earlier forward of this problem filled ``plan`` for
+    these cu_seqlens, unchanged since: its lists are reused (no list-building
+    launch)."""
     total_q, H, D = q.shape
     total_k, H_KV = k.shape[0], k.shape[1]
     H_G = 0 if r_q is None else r_q.shape[1]
@@ -325,7 +331,7 @@ def _fna2_forward_varlen(
     prob = _problem(True, N, max_seqlen_q, max_seqlen_k, total_q, total_k, H, H_KV, H_G, D, R,
                     is_causal, softmax_scale, cu_q, cu_k, dtype=q.dtype)
     _run_fwd(prob, q, k, v, r_q if H_G else None, r_k if H_G else None, gs, out, lse, _view3,
-             plan)
+             plan, plan_filled)
     return out, lse
 
 
@@ -410,6 +416,42 @@ def _plan_for(q, k, r_q, cu_q, cu_k, max_q, max_k, is_causal, scale):
     return new_plan(prob, q.device)
 
 
+# Plans of recent varlen forwards, by the cu_seqlens tensors they were built
+# for.  The tile lists depend only on the sequence extents and the problem's
+# shape, so a forward handed the very same cu_seqlens tensors (the layers of
+# one model step share them), unchanged since (torch bumps a tensor's version
+# counter on every in-place write), reuses the plan and launches no builder.
+# The entries hold the cu_seqlens tensors, so their memory cannot be reused by
+# other tensors while the entry lives.
+_PLANS: "collections.OrderedDict" = collections.OrderedDict()
+_PLANS_MAX = 8
+
+
+def _plan_reused(q, k, r_q, cu_q, cu_k, max_q, max_k, is_causal, scale):
+    """(plan, filled): the plan buffer of a varlen forward, and whether an
+    earlier forward filled it for these cu_seqlens tensors (same objects and
+    version counters, same device, stream and problem shape)."""
+    direct = all(t.dtype == torch.int32 and t.is_contiguous() and t.device == q.device
+                 for t in (cu_q, cu_k))
+    if not direct:  # the launcher converts them: a new tensor every call
+        return _plan_for(q, k, r_q, cu_q, cu_k, max_q, max_k, is_causal, scale), False
+    H_G = 0 if r_q is None else r_q.shape[1]
+    R = 0 if r_q is None else r_q.shape[2]
+    key = (q.device, _stream(q.device), id(cu_q), cu_q._version, id(cu_k), cu_k._version,
+           cu_q.shape[0], q.shape[0], k.shape[0], q.shape[1], k.shape[1], H_G, q.shape[2], R,
+           bool(is_causal))
+    hit = _PLANS.get(key)
+    if hit is not None and hit[0] is cu_q and hit[1] is cu_k:
+        _PLANS.move_to_end(key)
+        return hit[2], True
+    plan = _plan_for(q, k, r_q, cu_q, cu_k, max_q, max_k, is_causal, scale)
+    if plan is not None:
+        _PLANS[key] = (cu_q, cu_k, plan)
+        while len(_PLANS) > _PLANS_MAX:
+            _PLANS.popitem(last=False)
+    return plan, False
+
+
 def _dgs_out(d_gs, H_G, graph_scale):
     if not H_G or graph_scale is None:
         return None
@@ -439,13 +481,15 @@ class FlashNaylisAttnFunc(torch.autograd.Function):
             if cu_seqlens_k is None:
                 cu_seqlens_k = cu_seqlens_q
             # The forward's list-building launch also builds the backward's
-            # lists (kept on ctx): the backward then launches no builder.
-            plan = _plan_for(q, k, r_q, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
-                             max_seqlen_k, is_causal, softmax_scale)
+            # lists (kept on ctx): the backward then launches no builder; and
+            # a forward given the same cu_seqlens tensors again (the next
+            # layer) reuses them and launches none either.
+            plan, filled = _plan_reused(q, k, r_q, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                                        max_seqlen_k, is_causal, softmax_scale)
             out, lse = _fna2_forward_varlen(
                 q, k, v, r_q, r_k, graph_scale,
                 cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
-                softmax_scale, is_causal, plan=plan, lse_head_major=True,
+                softmax_scale, is_causal, plan=plan, lse_head_major=True, plan_filled=filled,
             )
             ctx.plan = plan
         else:

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define FNA2_ABI_VERSION 2
+#define FNA2_ABI_VERSION 3
 
 /* Element types.  The attention entry points (fna2_fwd, fna2_bwd,
  * fna2_fwd_noalloc) take FNA2_BF16 or FNA2_F16 for q, k, v, out, dout, dq,
@@ -117,6 +117,14 @@ typedef struct fna2_fwd_args {
    * problem) launches no builder: one launch fewer per training step. */
   void* plan;
   size_t plan_bytes;
+  /* Nonzero: `plan` was filled by an earlier fna2_fwd of this problem with
+   * cu_seqlens of unchanged contents (the caller's guarantee; ordered before
+   * this call on the stream), so its lists are reused and this call launches
+   * no builder (e.g. the layers of one model step, which share cu_seqlens).
+   * The library still checks that its record of the plan matches the
+   * problem (sizes, causal flag, cu_seqlens pointers, key-tile size) and
+   * builds the lists when it does not.  0: build them. */
+  int32_t plan_filled;
 } fna2_fwd_args;
 
 #define FNA2_FWD_EVENTS 2 /* attention kernel start, end */

@@ -45,7 +45,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_version_and_status_strings(lib):
-    assert lib.fna2_version() == 2
+    assert lib.fna2_version() == 3
     for code in _capi.STATUS:
         assert lib.fna2_status_string(code)
     assert lib.fna2_status_string(12345) == b"unknown status"

@@ -390,6 +390,67 @@ def test_plan_of_another_key_tile_size_is_ignored(gpu):
     H.check_grads(with_plan, ref_g)
 
 
+def test_plan_reused_across_calls_with_the_same_cu_seqlens(gpu):
+    """The autograd path reuses a plan for cu_seqlens tensors it saw
+    unchanged (the layers of one step): the second call launches no builder
+    and its results equal a fresh call's; an in-place write to cu_seqlens
+    (new lengths) bumps its version, and the plan is rebuilt."""
+    F = _fna2()
+    F._PLANS.clear()
+    lengths = [200, 1, 77, 300]
+    (q, k, v, rq, rk, gs_, dout, cu_q, cu_k) = H.make_varlen(lengths, 4, 128, 2, 4, 32, seed=40)
+    g = [t.to(gpu) for t in (q, k, v, rq, rk, gs_, dout)]
+    cu = cu_q.to(gpu)
+
+    def run(c, mx):
+        leaves = [t.detach().requires_grad_(True) for t in g[:6]]
+        out = F.flash_naylis_attn(*leaves, softmax_scale=0.1, is_causal=True, cu_seqlens_q=c,
+                                  cu_seqlens_k=c, max_seqlen_q=mx, max_seqlen_k=mx)
+        return [out.detach()] + [x.detach() for x in torch.autograd.grad(out, leaves, g[6])]
+
+    print("plan reuse: first call builds, second reuses", flush=True)
+    first = run(cu, 300)
+    assert len(F._PLANS) == 1
+    second = run(cu, 300)
+    torch.cuda.synchronize()
+    for a, b in zip(first, second):
+        assert torch.equal(a, b)
+    out, lse = F._fna2_forward_varlen(*g[:6], cu, cu, 300, 300, 0.1, True)
+    ref = F._fna2_backward_varlen(g[6], *g[:6], out, lse, cu, cu, 300, 300, 0.1, True)
+    torch.cuda.synchronize()
+    assert torch.equal(second[0], out)
+    for a, b in zip(second[1:], ref):
+        assert torch.equal(a, b)
+    # new lengths written in place: the cached plan must not be used
+    lengths2 = [50, 350, 1, 177]
+    cu.copy_(torch.tensor([0] + list(np.cumsum(lengths2)), dtype=torch.int32, device=gpu))
+    print("plan reuse: cu_seqlens rewritten in place", flush=True)
+    third = run(cu, 350)
+    torch.cuda.synchronize()
+    cu2 = cu.cpu().numpy()
+    ref_out, ref_lse, ref_g = H.oracle_fwd_bwd(q, k, v, rq, rk, gs_, dout, 0.1, True, cu2, cu2)
+    H.check_out(third[0], None, ref_out, ref_lse)
+    H.check_grads(third[1:], ref_g)
+
+
+def test_plan_filled_flag_on_a_plan_no_forward_filled_is_ignored(gpu):
+    """plan_filled with a plan the library has no record of filling for this
+    problem (garbage): the forward builds the lists anyway."""
+    F = _fna2()
+    lengths = [70, 3, 200, 129]
+    (q, k, v, rq, rk, gs_, dout, cu_q, cu_k) = H.make_varlen(lengths, 4, 128, 2, 4, 32, seed=41)
+    g = [t.to(gpu) for t in (q, k, v, rq, rk, gs_, dout, cu_q, cu_k)]
+    plan = F._plan_for(g[0], g[1], g[3], g[7], g[8], 200, 200, True, 0.09)
+    plan.fill_(0xAB)
+    print("plan_filled on an unfilled plan", flush=True)
+    out, lse = F._fna2_forward_varlen(*g[:6], g[7], g[8], 200, 200, 0.09, True, plan=plan,
+                                      plan_filled=True)
+    torch.cuda.synchronize()
+    ref_out, ref_lse, _ = H.oracle_fwd_bwd(q, k, v, rq, rk, gs_, dout, 0.09, True,
+                                           cu_q.numpy(), cu_k.numpy(), backward=False)
+    H.check_out(out, lse, ref_out, ref_lse)
+
+
 def test_varlen_lse_layout_matches_reference(gpu):
     """_fna2_forward_varlen returns lse as a contiguous [T, H] tensor, as the
     reference allocates it (flash_naylis_attn.py:780), with the same values
