@@ -64,6 +64,9 @@ def parse():
                     help="measure the varlen RoPE kernel (c3 pack) instead of attention")
     ap.add_argument("--decode", action="store_true",
                     help="bench the KV-cache decode kernel instead of the training step")
+    ap.add_argument("--leg", choices=["all", "fused", "separate"], default="all",
+                    help="--producer: run only the one-GEMM legs or only the five projections "
+                         "(e.g. to trace one of them alone)")
     ap.add_argument("--producer", action="store_true",
                     help="measure the fused operand projection (c3-sized module) instead")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
@@ -532,8 +535,11 @@ def producer_bench(args):
         torch.autograd.grad(outs, [x] + params, cot)
 
     res = {}
-    for name, fn, cot in (("separate", separate, grads), ("fused", lambda: m._project(x), grads),
-                          ("fused_stacked_grads", lambda: m._project(x), stacked)):
+    legs = (("separate", separate, grads), ("fused", lambda: m._project(x), grads),
+            ("fused_stacked_grads", lambda: m._project(x), stacked))
+    if args.leg != "all":
+        legs = [leg for leg in legs if leg[0].startswith(args.leg)]
+    for name, fn, cot in legs:
         run_ = lambda: run(fn, cot)
         for _ in range(args.warmup):
             run_()
@@ -547,6 +553,9 @@ def producer_bench(args):
         res[name] = e0.elapsed_time(e1) / args.steps
     n_all = E + 2 * H * D + 2 * HG * R
     flops = 3 * 2 * T * E * n_all  # forward GEMM, dX and dW GEMMs
+    if "fused" not in res:  # --leg separate
+        print(json.dumps({"separate_ms": round(res["separate"], 4)}), flush=True)
+        return
     tf = flops / (res["fused"] * 1e-3) / 1e12
     print(json.dumps({
         "metric": "operand producer fwd+bwd TFLOP/s (one GEMM over stacked q/k/v/R weights)",
@@ -558,8 +567,9 @@ def producer_bench(args):
         "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4),
                      "traffic": None, "kernel": "hipBLASLt GEMMs"},
-        "separate_ms": round(res["separate"], 4),
-        "speedup_over_separate": round(res["separate"] / res["fused"], 3),
+        "separate_ms": round(res["separate"], 4) if "separate" in res else None,
+        "speedup_over_separate": (round(res["separate"] / res["fused"], 3)
+                                  if "separate" in res else None),
         "ms_stacked_grads": round(res["fused_stacked_grads"], 4),
         "cpu_baseline": None,
     }), flush=True)

@@ -42,9 +42,19 @@ struct FwdCfg {
   static constexpr int STAGE = KBYTES + RBYTES + VBYTES;
 };
 
-template <int D, int RPL, bool F16>
+// S16 (R <= 16, rank tile 32): the rank chain accumulates b <Rq, Rk>
+// directly.  The query's rank operand holds b Rq split in two bf16 parts,
+// hi = bf16(b Rq) in features 0..15 and lo = bf16(b Rq - hi) in features
+// 16..31 of the tile, and the key-side tile holds Rk in both halves (its DMA
+// mirrors chunks 0..1 into 2..3): the two 16-deep rank steps then sum to
+// <hi + lo, Rk>, b <Rq, Rk> to 2^-16 (the products exact in fp32), and the
+// score tile needs no scaling by b -- 16 VALU multiplies fewer per 32 x 32
+// tile for one more MFMA, and no register more (the halves are the padding
+// of the rank tile).
+template <int D, int RPL, bool F16, bool S16>
 __device__ __forceinline__ void fwd_body(const FwdParams& P) {
   using C = FwdCfg<D, RPL>;
+  static_assert(!S16 || RPL == 32, "the split uses the padding of a 32-wide rank tile");
   // Two stages as separate objects: the compiler can then tell that reads of
   // one stage never alias the DMA into the other and does not wait for it.
   __shared__ __attribute__((aligned(1024))) uint8_t stage0[C::STAGE];
@@ -69,7 +79,7 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
   const int kvh = h / p.group;
   const bool graph = (RPL > 0) && (h < p.H_G);
   const float bh = uni_f(graph ? *const_space(P.gs + h) / p.c : 0.f);
-  const int nrs = graph ? cdiv(p.R, 16) : 0;  // rank steps actually used
+  const int nrs = graph ? (S16 ? 2 : cdiv(p.R, 16)) : 0;  // rank steps actually used
 
   const uint16_t* qb = seq_base<const uint16_t>(P.q, p, b, e.q0, h);
   const uint16_t* kb = seq_base<const uint16_t>(P.k, p, b, e.k0, kvh);
@@ -97,7 +107,7 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
   if constexpr (C::CR > 0) {
     rkrb = (uint32_t)P.rk.ss * 2u;
     if (graph) rkb = seq_base<const uint16_t>(P.rk, p, b, e.k0, h);
-    dr.init(wv, lane, rkrb, p.R / 8);
+    dr.init(wv, lane, rkrb, p.R / 8, S16);
   }
   auto issue = [&](int kt, uint8_t* base) {
     const int k0 = kt * C::BN;
@@ -140,6 +150,19 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
         qreg[C::KSD + s] =
             as_bf16x8(__builtin_amdgcn_raw_buffer_load_b128(rr, in ? ro + 32u * s : kOOB, 0, 0));
       }
+      if constexpr (S16) {
+        // this lane's features 8 hl .. +7 (step 0): hi there, lo in step 1
+        const u32x4 r = as_u32x4(qreg[C::KSD]);
+        u32x4 hi, lo;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float x0 = bf16_lo(r[i]) * bh, x1 = bf16_hi(r[i]) * bh;
+          hi[i] = pack_bf16(x0, x1);
+          lo[i] = pack_bf16(x0 - bf16_lo(hi[i]), x1 - bf16_hi(hi[i]));
+        }
+        qreg[C::KSD] = as_bf16x8(hi);
+        qreg[C::KSD + 1] = as_bf16x8(lo);
+      }
     }
   }
 
@@ -173,7 +196,7 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
 #pragma unroll
         for (int s = 0; s < C::KSR; ++s)
           if (s < nrs) acc = mfma32(row_read<C::BN>(rl, rdl, kb2 * 32, s), qreg[C::KSD + s], acc);
-        acc *= bh;
+        if constexpr (!S16) acc *= bh;
       }
 #pragma unroll
       for (int s = 0; s < C::KSD; ++s)
@@ -287,20 +310,21 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
 // One non-template kernel per (D, padded rank, element type): every kernel
 // gets its own host launch stub.  WAVES: waves per SIMD the register budget
 // is cut for.
-#define FNA2_FWD_KERNEL(D, RPL, WAVES)                                                      \
-  __global__ __launch_bounds__(256, WAVES) void fwd_kernel_d##D##_r##RPL(const FwdParams P) { \
-    fwd_body<D, RPL, false>(P);                                                             \
-  }                                                                                         \
-  __global__ __launch_bounds__(256, WAVES) void fwd_kernel_d##D##_r##RPL##_f16(               \
-      const FwdParams P) {                                                                  \
-    fwd_body<D, RPL, true>(P);                                                              \
+#define FNA2_FWD_KERNEL(D, RNAME, RPL, S16, WAVES)                                          \
+  __global__ __launch_bounds__(256, WAVES) void fwd_kernel_d##D##_r##RNAME(const FwdParams P) { \
+    fwd_body<D, RPL, false, S16>(P);                                                         \
+  }                                                                                          \
+  __global__ __launch_bounds__(256, WAVES) void fwd_kernel_d##D##_r##RNAME##_f16(              \
+      const FwdParams P) {                                                                   \
+    fwd_body<D, RPL, true, S16>(P);                                                          \
   }
-FNA2_FWD_KERNEL(64, 0, 2)
-FNA2_FWD_KERNEL(64, 32, 2)
-FNA2_FWD_KERNEL(64, 64, 2)
-FNA2_FWD_KERNEL(128, 0, 3)
-FNA2_FWD_KERNEL(128, 32, 3)
-FNA2_FWD_KERNEL(128, 64, 3)
+FNA2_FWD_KERNEL(64, 0, 0, false, 2)
+FNA2_FWD_KERNEL(64, 16, 32, true, 2)
+FNA2_FWD_KERNEL(64, 32, 32, false, 2)
+FNA2_FWD_KERNEL(64, 64, 64, false, 2)
+FNA2_FWD_KERNEL(128, 0, 0, false, 3)
+FNA2_FWD_KERNEL(128, 32, 32, false, 3)
+FNA2_FWD_KERNEL(128, 64, 64, false, 3)
 #undef FNA2_FWD_KERNEL
 
 }  // namespace
@@ -308,13 +332,19 @@ FNA2_FWD_KERNEL(128, 64, 3)
 hipError_t launch_fwd(const FwdParams& P, int rpl, int grid, hipStream_t s) {
   if (grid <= 0) return hipSuccess;
   void (*k)(const FwdParams) = nullptr;
+  // d = 64 with R <= 16: the split rank operand (S16)
+  const bool r16 = rpl == 32 && P.p.R <= 16;
   if (P.p.f16) {
     if (P.p.D == 64)
-      k = rpl == 0 ? fwd_kernel_d64_r0_f16 : rpl == 32 ? fwd_kernel_d64_r32_f16 : fwd_kernel_d64_r64_f16;
+      k = rpl == 0 ? fwd_kernel_d64_r0_f16
+          : rpl == 32 ? (r16 ? fwd_kernel_d64_r16_f16 : fwd_kernel_d64_r32_f16)
+                      : fwd_kernel_d64_r64_f16;
     if (P.p.D == 128)
       k = rpl == 0 ? fwd_kernel_d128_r0_f16 : rpl == 32 ? fwd_kernel_d128_r32_f16 : fwd_kernel_d128_r64_f16;
   } else {
-    if (P.p.D == 64) k = rpl == 0 ? fwd_kernel_d64_r0 : rpl == 32 ? fwd_kernel_d64_r32 : fwd_kernel_d64_r64;
+    if (P.p.D == 64)
+      k = rpl == 0 ? fwd_kernel_d64_r0
+          : rpl == 32 ? (r16 ? fwd_kernel_d64_r16 : fwd_kernel_d64_r32) : fwd_kernel_d64_r64;
     if (P.p.D == 128) k = rpl == 0 ? fwd_kernel_d128_r0 : rpl == 32 ? fwd_kernel_d128_r32 : fwd_kernel_d128_r64;
   }
   if (!k || (rpl != 0 && rpl != 32 && rpl != 64)) return hipErrorInvalidValue;

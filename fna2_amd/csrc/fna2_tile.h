@@ -133,20 +133,24 @@ struct Dma {
 
   // row_bytes: tensor row stride in bytes; valid_chunks: chunks with data
   // (features / 8); chunks past it read zeros.
-  __device__ __forceinline__ void init(int wave, int lane, uint32_t row_bytes, int valid_chunks) {
+  __device__ __forceinline__ void init(int wave, int lane, uint32_t row_bytes, int valid_chunks,
+                                       bool mirror = false) {
 #pragma unroll
     for (int j = 0; j < PER_WAVE; ++j)
-      voff[j] = slot_offset(wave + j * NWAVE, lane, row_bytes, valid_chunks);
+      voff[j] = slot_offset(wave + j * NWAVE, lane, row_bytes, valid_chunks, mirror);
   }
 
-  // Global byte offset of the chunk that lands in slot 64 i + lane.
+  // Global byte offset of the chunk that lands in slot 64 i + lane.  With
+  // `mirror` (a 4-chunk row holding at most 2 chunks of data), chunks 2 and
+  // 3 load the data of chunks 0 and 1 again.
   __device__ __forceinline__ static uint32_t slot_offset(int i, int lane, uint32_t row_bytes,
-                                                         int valid_chunks) {
+                                                         int valid_chunks, bool mirror = false) {
     const int p = 64 * i + lane;
     const int grp = p / (ROWS * 4);
     const int rem = p - grp * (ROWS * 4);
     const int row = rem >> 2;
-    const int col = 4 * grp + ((rem & 3) ^ swz4(row));
+    int col = 4 * grp + ((rem & 3) ^ swz4(row));
+    if (mirror) col &= 1;
     return (i < N && col < valid_chunks) ? (uint32_t)row * row_bytes + (uint32_t)col * 16u : kOOB;
   }
 
