@@ -185,6 +185,39 @@ def test_fna2_varlen_matches_dense_per_sequence(gpu):
         off += n
 
 
+@pytest.mark.gpu
+def test_fp16_module_fna2_matches_fp32_eager(gpu):
+    """An fp16 NaylisAttention (the reference runs its FNA2 kernels on fp16
+    q/k/v too): its FNA2 path, dense and varlen, against the same module's
+    eager path in fp32 on the CPU, forward and parameter gradients."""
+    assert A._FNA2_AVAILABLE
+    ref, fast = _pair(embed_dim=512, num_heads=4, n_kv_heads=2, rel_rank=16, vanilla_heads=1)
+    fast = fast.half()
+    x = torch.randn(2, 150, 512)
+    y_ref, _ = ref(x)
+    y_fast, _ = fast(x.half().cuda())
+    assert y_fast.dtype == torch.float16
+    assert (y_fast.float().cpu() - y_ref).abs().max().item() < 2e-2
+    g = torch.randn_like(y_ref)
+    gr = torch.autograd.grad(y_ref, list(ref.parameters()), g)
+    gf = torch.autograd.grad(y_fast, list(fast.parameters()), g.half().cuda())
+    for (name, _), a, b in zip(ref.named_parameters(), gr, gf):
+        rel = ((a - b.float().cpu()).norm() / a.norm().clamp_min(1e-6)).item()
+        assert rel < 5e-2, (name, rel)
+    # varlen: each sequence equals the dense eager path on that sequence
+    lens = [37, 128, 5, 90]
+    xv = torch.randn(sum(lens), 512)
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32,
+                      device="cuda")
+    yv, _ = fast(xv.half().cuda(), cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=max(lens),
+                 max_seqlen_k=max(lens))
+    off = 0
+    for n in lens:
+        yd, _ = ref(xv[off:off + n][None])
+        assert (yv[off:off + n].float().cpu() - yd[0]).abs().max().item() < 2e-2
+        off += n
+
+
 @pytest.mark.parametrize("lead", [(37,), (2, 19)])
 def test_fused_projection_equals_separate_projections(lead):
     """One GEMM over the stacked weights gives the five projections
