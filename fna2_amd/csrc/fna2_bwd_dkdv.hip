@@ -27,8 +27,8 @@
 // and neither role needs more than half of the SIMD's registers.  dK and dV
 // accumulate over the whole GQA group in fp32: no atomics.
 //
-// The dQ kernel stores a head-major copy of Rq together with delta and
-// -LSE log2(e); the sign/zero factor a of the augmented query rides on the
+// The dQ kernel stores delta and -LSE log2(e) (Rq is read where the caller
+// holds it); the sign/zero factor a of the augmented query rides on the
 // stationary K (exact), and S is formed as the forward forms it (the rank
 // chain scaled by b = graph_scale[h] / c in fp32, then the head-dim chain),
 // so the recomputed S equals the forward's bit for bit.
@@ -178,10 +178,11 @@ struct RingDma {
   __device__ __forceinline__ void init(const BwdParams& P, int w, int lane) {
     qrb = (uint32_t)P.q.ss * 2u;
     orb = (uint32_t)P.dout.ss * 2u;
-    srb = (uint32_t)P.rqs.ss * 2u;
+    srb = (uint32_t)P.rq.ss * 2u;
     if constexpr ((MASK & kTileQ) != 0) dmq.init_fixed(w, lane, qrb, C::CD);
     if constexpr ((MASK & kTileO) != 0) dmo.init_fixed(w, lane, orb, C::CD);
-    if constexpr ((MASK & kTileR) != 0 && RPL > 0) dmr.init_fixed(w, lane, srb, C::CR);
+    // rank chunks past R read as zeros (past them lies the next head's rank)
+    if constexpr ((MASK & kTileR) != 0 && RPL > 0) dmr.init_fixed(w, lane, srb, P.p.R / 8);
     is_delta = (w & 1) != 0;
     lrb = (uint32_t)P.nlse.ss * 4u;
     drb = (uint32_t)P.delta.ss * 4u;
@@ -202,7 +203,7 @@ struct RingDma {
       so = rsrc_words(seq_base<const uint16_t>(view_of(&pp->dout), p, b, q0, h), lq * orb);
     if constexpr ((MASK & kTileR) != 0 && RPL > 0) {
       const bool graph = h < p.H_G;
-      sr = rsrc_words(graph ? seq_base<const uint16_t>(view_of(&pp->rqs), p, b, q0, h) : qb,
+      sr = rsrc_words(graph ? seq_base<const uint16_t>(view_of(&pp->rq), p, b, q0, h) : qb,
                       graph ? lq * srb : 0u);
     }
     if constexpr ((MASK & kTileL) != 0) {

@@ -6,8 +6,8 @@
 // One workgroup = 4 waves = 128 queries of one (sequence, head); wave w owns
 // queries 32w..32w+31 with Qa = [a Q | Rq] and dO rows in registers.
 // The prologue also forms delta = sum_d O dO for these queries (fp32); the
-// epilogue stores it, -LSE log2(e) and a head-major copy of Rq for the dK/dV
-// kernel, which runs after this one.
+// epilogue stores it and -LSE log2(e) for the dK/dV kernel, which runs after
+// this one.
 // Per key step (keys stream in by DMA through a two-stage ring):
 //   S^T, dP^T  (keys x 32 queries)      A operands: K | Rk and V rows (LDS)
 //   dS^T = P^T (dP^T - delta)
@@ -390,22 +390,12 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
                 P.drq.ss, nrows, p.R / 8, lane);
     }
   }
-  // For the dK/dV kernel: delta, -LSE log2(e) and the head-major copy of Rq
-  // (32 rows of one head per block, padded to the rank tile width with
-  // zeros).  They are stored here rather than in the prologue, where the
-  // first ring barrier (vmcnt(0)) would wait for the writes to complete.
-  if (qvalid) {
-    if (hl == 0) {
-      seq_base<float>(P.delta, p, b, e.q0, h)[(int64_t)qrow * P.delta.ss] = dl;
-      seq_base<float>(P.nlse, p, b, e.q0, h)[(int64_t)qrow * P.nlse.ss] = -lse2;
-    }
-    if constexpr (C::KSR > 0) {
-      if (graph) {
-        uint16_t* srow = seq_base<uint16_t>(P.rqs, p, b, e.q0, h) + (int64_t)qrow * P.rqs.ss;
-#pragma unroll
-        for (int s = 0; s < C::KSR; ++s) st16(srow + 16 * s + 8 * hl, as_u32x4(qreg[C::KSD + s]));
-      }
-    }
+  // For the dK/dV kernel: delta and -LSE log2(e).  They are stored here
+  // rather than in the prologue, where the first ring barrier (vmcnt(0))
+  // would wait for the writes to complete.
+  if (qvalid && hl == 0) {
+    seq_base<float>(P.delta, p, b, e.q0, h)[(int64_t)qrow * P.delta.ss] = dl;
+    seq_base<float>(P.nlse, p, b, e.q0, h)[(int64_t)qrow * P.nlse.ss] = -lse2;
   }
   // d_gs partial of this wave: sum_i <Rq_i, (dS Rk)_i> over its queries.
   if constexpr (C::NRB > 0) {

@@ -133,7 +133,7 @@ FwdWs fwd_ws(const fna2_problem& p) {
 }
 
 struct BwdWs {
-  size_t tiles_q = 0, count_q = 0, tiles_k = 0, count_k = 0, partial = 0, rqs = 0, nlse = 0;
+  size_t tiles_q = 0, count_q = 0, tiles_k = 0, count_k = 0, partial = 0, nlse = 0;
   size_t bytes = 0;
 };
 BwdWs bwd_ws(const fna2_problem& p) {
@@ -154,10 +154,6 @@ BwdWs bwd_ws(const fna2_problem& p) {
   // d_gs partials: [query tiles][4 waves][H_G]
   off += align_up(sizeof(float) * 4u * (size_t)(g.q_tiles > 0 ? g.q_tiles : 1) *
                   (size_t)(p.heads_graph > 0 ? p.heads_graph : 1));
-  // bf16(graph_scale / c * Rq), [H_G][rows_q][rank width] (per batch)
-  w.rqs = off;
-  const int rpl = fna2::padded_rank32(p.heads_graph, p.rank);
-  off += align_up((size_t)rows_q(p) * (size_t)p.heads_graph * (size_t)rpl * 2u);
   // -LSE log2(e), fp32 [H][rows_q] (per batch)
   w.nlse = off;
   off += align_up((size_t)rows_q(p) * (size_t)p.heads * 4u);
@@ -568,13 +564,9 @@ int fna2_bwd(const fna2_bwd_args* a, void* stream_ptr) {
   K.q_tiles = (int)g.q_tiles;
   K.k_tiles = (int)g.kv_tiles;
   const int rpl = fna2::padded_rank32(K.p.H_G, K.p.R);
-  // Both are head-major (a head's rows are contiguous): the dK/dV kernel
-  // reads them per head, 32 rows at a time.
+  // Head-major (a head's rows are contiguous): the dK/dV kernel reads it per
+  // head, 32 rows at a time.
   const int64_t seq_rows = p.varlen ? (int64_t)p.total_q : (int64_t)p.seqlen_q;
-  K.rqs.ptr = (char*)a->workspace + w.rqs;
-  K.rqs.ss = rpl;
-  K.rqs.sh = seq_rows * rpl;
-  K.rqs.sb = p.varlen ? 0 : (int64_t)p.heads_graph * K.rqs.sh;
   K.nlse.ptr = (char*)a->workspace + w.nlse;
   K.nlse.ss = 1;
   K.nlse.sh = seq_rows;

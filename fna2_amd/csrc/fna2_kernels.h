@@ -17,7 +17,6 @@ struct BwdParams {
   Problem p;
   TView q, k, v, rq, rk, o, lse, dout, delta, dq, dk, dv, drq, drk;
   // Workspace written by the dQ kernel for the dK/dV kernel:
-  TView rqs;   // Rq, head-major [H_G][rows][rank width] (zero padding)
   TView nlse;  // -LSE log2(e), fp32 [H][rows]
   const float* gs;
   float* dgs;            // [H_G]

@@ -200,9 +200,6 @@ def model_dq(m, P, T, W):
                 for name in ("delta", "nlse"):
                     t = T[name] if name == "delta" else W["nlse"]
                     m.rows(t, m.base(t, b, q0, h) + q0t * t.ss * 4, qrows, 4, "dq " + name)
-                if graph and rpl > 0:
-                    rqs = W["rqs"]
-                    m.rows(rqs, m.base(rqs, b, q0, h) + q0t * rqs.ss * 2, qrows, 2 * rpl, "dq rqs")
                 if graph:
                     part = W["partial"]
                     for wv in range(4):
@@ -253,10 +250,10 @@ def model_dkdv(m, P, T, W, rank_read="R"):
                         t = T[name]
                         m.rows(t, m.base(t, b, q0, h) + r0 * t.ss * t.es, n, 2 * D,
                                "dkdv " + name)
-                    if graph:
-                        rqs = W["rqs"]
-                        m.rows(rqs, m.base(rqs, b, q0, h) + r0 * rqs.ss * 2, n, 2 * rpl,
-                               "dkdv rqs")
+                    if graph:  # rank chunks past R read at an out-of-range offset
+                        rq = T["rq"]
+                        m.rows(rq, m.base(rq, b, q0, h) + r0 * rq.ss * rq.es, n, 2 * R,
+                               "dkdv rq")
                     for t in (T["delta"], W["nlse"]):
                         m.rows(t, m.base(t, b, q0, h) + r0 * t.ss * 4, n, 4, "dkdv " + t.name)
 
@@ -277,8 +274,6 @@ def workspace(P, lib, prob, device="cpu"):
         q_tiles = P["B"] * cdiv(P["sq"], 128)
     partial = off
     off += align_up(4 * 4 * max(q_tiles, 1) * max(H_G, 1))
-    rqs = off
-    off += align_up(rows_q * H_G * rpl * 2)
     nlse = off
     off += align_up(rows_q * H * 4)
     assert off == lib.fna2_bwd_workspace_bytes(ctypes.byref(prob)), "bwd_ws restatement"
@@ -292,7 +287,6 @@ def workspace(P, lib, prob, device="cpu"):
         return V(name, st, es, lo, hi)
 
     W = {"partial": mk("partial", partial, 1, 0, 0, 4),
-         "rqs": mk("rqs", rqs, rpl, seq_rows * rpl, 0 if P["varlen"] else H_G * seq_rows * rpl, 2),
          "nlse": mk("nlse", nlse, 1, seq_rows, 0 if P["varlen"] else H * seq_rows, 4)}
     # the partials region: [q_tiles][4][H_G] floats
     W["partial"].hi = base + partial + 4 * 4 * max(q_tiles, 1) * max(H_G, 1)
