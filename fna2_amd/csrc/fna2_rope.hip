@@ -105,6 +105,26 @@ struct Chunk {
   }
 };
 
+// 16 bytes as loaded (EPL elements), unpacked on use: rows in flight cost
+// half the registers of their fp32 values.
+template <int DT>
+struct Raw {
+  static constexpr int EPL = Chunk<DT>::EPL;
+  u32x4 w;
+  __device__ __forceinline__ void load(const void* p) { w = *(const u32x4*)p; }
+  __device__ __forceinline__ void store(void* p) const { *(u32x4*)p = w; }
+  __device__ __forceinline__ float get(int e) const {
+    if constexpr (DT == kRopeF32) {
+      return __builtin_bit_cast(float, (uint32_t)w[e]);
+    } else if constexpr (DT == kRopeBF16) {
+      return (e & 1) ? bf16_hi(w[e >> 1]) : bf16_lo(w[e >> 1]);
+    } else {
+      const uint32_t u = w[e >> 1];
+      return (float)__builtin_bit_cast(_Float16, (uint16_t)((e & 1) ? (u >> 16) : (u & 0xffffu)));
+    }
+  }
+};
+
 // Lane layout and the token -> sequence walk shared by the kernels: lane
 // owns columns [col, col + EPL) of both halves of row lrow + j * rpw of a
 // token; a wave covers kRopeTokensPerWave consecutive tokens from t0.
@@ -171,21 +191,21 @@ __global__ __launch_bounds__(64 * kRopeWaves) void rope_kernel(const RopeParams 
   constexpr int ES = DT == kRopeF32 ? 4 : 2;
   constexpr int TD = NORM ? kRopeF32 : DT;  // type of the table and of the rotation
   RopeLanes<DT> L(P, blockIdx.x * kRopeWaves + uni(threadIdx.x >> 6));
-  if (L.t0 >= P.T) return;
+  // (no early return before the weights' barrier: a wave past the last
+  // token runs no token iteration below)
   const int col = L.col, half = L.half;
 
   float invf[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) invf[e] = rnd<TD>(P.inv_freq[col + e]);
-  float wq1[NORM ? EPL : 1], wq2[NORM ? EPL : 1], wk1[NORM ? EPL : 1], wk2[NORM ? EPL : 1];
+  // the norm weights (q, k), in LDS rather than in every lane's registers
+  __shared__ float wsh[NORM ? 2 : 1][NORM ? 512 : 1];
   if constexpr (NORM) {
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      wq1[e] = P.wq ? P.wq[col + e] : 1.f;
-      wq2[e] = P.wq ? P.wq[half + col + e] : 1.f;
-      wk1[e] = P.wk ? P.wk[col + e] : 1.f;
-      wk2[e] = P.wk ? P.wk[half + col + e] : 1.f;
+    for (int d = threadIdx.x; d < P.D; d += 64 * kRopeWaves) {
+      wsh[0][d] = P.wq ? P.wq[d] : 1.f;
+      wsh[1][d] = P.wk ? P.wk[d] : 1.f;
     }
+    __syncthreads();
   }
   const float inv_d = 1.f / (float)P.D;
 
@@ -210,7 +230,8 @@ __global__ __launch_bounds__(64 * kRopeWaves) void rope_kernel(const RopeParams 
     // the stores.  (With the norm every lane makes the same passes: the row
     // sums cross lanes.)
     for (int r0 = L.lrow; (NORM ? r0 - L.lrow : r0) < L.nrows; r0 += kRopePasses * L.rpw) {
-      Ch x1[kRopePasses], x2[kRopePasses];
+      Raw<DT> x1[kRopePasses], x2[kRopePasses];
+      float rs[kRopePasses];  // the row's RMS factor (0: no norm)
       char* dst[kRopePasses];
       bool copy[kRopePasses], isq[kRopePasses];
 #pragma unroll
@@ -226,6 +247,8 @@ __global__ __launch_bounds__(64 * kRopeWaves) void rope_kernel(const RopeParams 
           x2[j].load(src + (half + col) * ES);
         }
       }
+#pragma unroll
+      for (int j = 0; j < kRopePasses; ++j) rs[j] = 0.f;
       if constexpr (NORM) {
         if (inside) {
           // RMS of each row (every lane joins the cross-lane sums)
@@ -234,18 +257,14 @@ __global__ __launch_bounds__(64 * kRopeWaves) void rope_kernel(const RopeParams 
             float ss = 0.f;
             if (dst[j]) {
 #pragma unroll
-              for (int e = 0; e < EPL; ++e) ss += x1[j].v[e] * x1[j].v[e] + x2[j].v[e] * x2[j].v[e];
+              for (int e = 0; e < EPL; ++e) {
+                const float a = x1[j].get(e), b2 = x2[j].get(e);
+                ss += a * a + b2 * b2;
+              }
             }
             ss = row_sum(ss, L.lpr);
             const bool has_w = isq[j] ? P.wq != nullptr : P.wk != nullptr;
-            if (dst[j] && has_w) {
-              const float rr = rsqrtf(ss * inv_d + P.eps);
-#pragma unroll
-              for (int e = 0; e < EPL; ++e) {
-                x1[j].v[e] = x1[j].v[e] * rr * (isq[j] ? wq1[e] : wk1[e]);
-                x2[j].v[e] = x2[j].v[e] * rr * (isq[j] ? wq2[e] : wk2[e]);
-              }
-            }
+            if (dst[j] && has_w) rs[j] = rsqrtf(ss * inv_d + P.eps);
           }
         }
       }
@@ -256,10 +275,14 @@ __global__ __launch_bounds__(64 * kRopeWaves) void rope_kernel(const RopeParams 
           Ch y1, y2;
 #pragma unroll
           for (int e = 0; e < EPL; ++e) {
-            y1.v[e] = rnd<TD>(add_rn(rnd<TD>(mul_rn(x1[j].v[e], c[e])),
-                                     rnd<TD>(mul_rn(-x2[j].v[e], s[e]))));
-            y2.v[e] = rnd<TD>(add_rn(rnd<TD>(mul_rn(x2[j].v[e], c[e])),
-                                     rnd<TD>(mul_rn(x1[j].v[e], s[e]))));
+            float a = x1[j].get(e), b2 = x2[j].get(e);
+            if (NORM && rs[j] != 0.f) {  // x r w, as (x r) w
+              const float* w = wsh[isq[j] ? 0 : 1];
+              a = a * rs[j] * w[col + e];
+              b2 = b2 * rs[j] * w[half + col + e];
+            }
+            y1.v[e] = rnd<TD>(add_rn(rnd<TD>(mul_rn(a, c[e])), rnd<TD>(mul_rn(-b2, s[e]))));
+            y2.v[e] = rnd<TD>(add_rn(rnd<TD>(mul_rn(b2, c[e])), rnd<TD>(mul_rn(a, s[e]))));
           }
           y1.store(dst[j] + col * ES);
           y2.store(dst[j] + (half + col) * ES);
