@@ -282,8 +282,17 @@ class _StackedProjection(torch.autograd.Function):
         dw_all = None
         if any(n and g is not None for n, g in zip(need_w, gys)):
             dw_all = torch.empty_like(w_all)
-        dws, r0 = [], 0
-        for g, n, need in zip(gys, sizes, need_w):
+        stacked = _column_blocks(gys, sizes)
+        if stacked is not None and all(need_w) and dw_all.dtype == cd:
+            # every block's dW in one GEMM: dW_all = dY_all^T x
+            torch.mm(stacked.t(), x2, out=dw_all)
+            gys_w = ()
+            dws = list(torch.split(dw_all, sizes, dim=0))
+        else:
+            gys_w = gys
+            dws = []
+        r0 = 0
+        for g, n, need in zip(gys_w, sizes, need_w):
             if g is None or not need:
                 dws.append(None)
             else:
@@ -296,7 +305,6 @@ class _StackedProjection(torch.autograd.Function):
             r0 += n
         dx = None
         if ctx.needs_input_grad[0]:
-            stacked = _column_blocks(gys, sizes)
             if stacked is not None:
                 dx = torch.mm(stacked, w_c)
             else:
