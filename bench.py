@@ -31,7 +31,13 @@ and the oracle on the host.
 (q, k, v, R_q, R_k from x: one GEMM over the stacked weights, forward and
 backward) against the reference's five separate projections.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3] [--rope|--producer]
+``--module`` measures one NaylisAttention layer's packed forward + backward
+on the c3 pack (projection, QK-RMSNorm + RoPE, attention, output
+projection), with the projection's gradients written into one buffer and,
+for comparison, into separate tensors.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3]
+                       [--rope|--producer|--module|--decode]
 """
 from __future__ import annotations
 
@@ -69,6 +75,9 @@ def parse():
                          "(e.g. to trace one of them alone)")
     ap.add_argument("--producer", action="store_true",
                     help="measure the fused operand projection (c3-sized module) instead")
+    ap.add_argument("--module", action="store_true",
+                    help="measure one NaylisAttention layer's packed forward + backward "
+                         "(c3 pack, E = 2048) instead")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU-baseline budget (seconds)")
     ap.add_argument("--no-flush", action="store_true",
@@ -575,6 +584,68 @@ def producer_bench(args):
     }), flush=True)
 
 
+def module_bench(args):
+    """One NaylisAttention layer on the c3 pack (16384 tokens / 64 sequences,
+    E = 2048, 16 heads of 128, 16 graph heads of rank 32, QK-RMSNorm, RoPE,
+    bf16), forward + backward of the packed path: the one-GEMM projection,
+    the norm + RoPE launch, the attention kernels and the output projection.
+    ``value``: with the projection's gradients written into one buffer
+    (GradSlab: one dx and one dW GEMM); ``separate_ms``: with separate
+    gradient tensors."""
+    import numpy as np
+    import torch
+
+    from fna2_amd import attention_fna2 as A
+    from fna2_amd import configs
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = configs.get("c3")
+    lens = cfg.seq_lengths()
+    T, E = sum(lens), 2048
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32, device=dev)
+    torch.manual_seed(0)
+    m = A.NaylisAttention(E, 16, rel_rank=32, max_seq_len=1024).to(device=dev,
+                                                                   dtype=torch.bfloat16)
+    assert A._FNA2_AVAILABLE, "the HIP library and a gfx950 device are needed"
+    m._use_fna2 = True
+    x = torch.randn(T, E, device=dev, dtype=torch.bfloat16, requires_grad=True)
+    g = torch.randn(T, E, device=dev, dtype=torch.bfloat16)
+
+    def step():
+        y, _ = m(x, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=max(lens),
+                 max_seqlen_k=max(lens))
+        y.backward(g)
+
+    res = {}
+    try:
+        for slab in (True, False):
+            A.NaylisAttention._grad_slab = slab
+            for _ in range(args.warmup):
+                step()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(args.steps):
+                step()
+            e1.record()
+            torch.cuda.synchronize()
+            res[slab] = e0.elapsed_time(e1) / args.steps
+    finally:
+        A.NaylisAttention._grad_slab = True
+    print(json.dumps({
+        "metric": "NaylisAttention packed layer fwd+bwd tokens/s (c3 pack, E=2048)",
+        "value": round(T / (res[True] * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(res[True], 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) x and output gradient, random-init weights)",
+        "config": {"workload": f"NaylisAttention(2048, 16, rel_rank=32): {T} tokens / "
+                               f"{len(lens)} seqs, QK-RMSNorm + RoPE, causal"},
+        "separate_grads_ms": round(res[False], 4),
+        "speedup_over_separate_grads": round(res[False] / res[True], 3),
+    }), flush=True)
+
+
 def decode_bench(args):
     """One-token decode against a KV cache, with c3's attention geometry
     (16 heads of 128, all graph heads of rank 32), 64 sequences x 4096
@@ -785,6 +856,9 @@ def main():
         return
     if args.producer:
         producer_bench(args)
+        return
+    if args.module:
+        module_bench(args)
         return
     if args.rope:
         rope_bench(args)

@@ -43,6 +43,8 @@ import torch.nn.functional as F
 
 from . import _capi
 from .flash_naylis_attn import BLOCK_R, flash_naylis_attn, rank_supported
+from .flash_naylis_attn import FlashNaylisAttnFunc as _FNA2Func
+from .flash_naylis_attn import _plain_eager as _fna2_plain_eager
 from .decode import decode_supported, flash_naylis_decode
 from .rope import rope_varlen
 
@@ -60,7 +62,19 @@ def _detect_fna2() -> bool:
 
 _FNA2_AVAILABLE = _detect_fna2()
 _FNA2_BLOCK_R = BLOCK_R
-_flash_naylis_attn = flash_naylis_attn
+
+
+def _attention(q, k, v, r_q, r_k, graph_scale, grad_slab=None, **kw):
+    """flash_naylis_attn, or (varlen, run eagerly, with a GradSlab) its
+    autograd function told to write dv, dR_q and dR_k into the slab."""
+    if grad_slab is None:
+        return flash_naylis_attn(q, k, v, r_q, r_k, graph_scale, **kw)
+    return _FNA2Func.apply(q, k, v, r_q, r_k, graph_scale, float(kw["softmax_scale"]),
+                           bool(kw["is_causal"]), kw["cu_seqlens_q"], kw["cu_seqlens_k"],
+                           int(kw["max_seqlen_q"]), int(kw["max_seqlen_k"]), grad_slab)
+
+
+_flash_naylis_attn = _attention
 
 # (k, v), or (k, v, r_k) for a module built with decode_graph_bias=True.
 KVCache = Tuple[torch.Tensor, ...]
@@ -192,11 +206,12 @@ class RotaryPositionalEmbedding(nn.Module):
     def forward_varlen(self, q: torch.Tensor, k: torch.Tensor, cu_seqlens: torch.Tensor,
                        norm_q: Optional[torch.Tensor] = None,
                        norm_k: Optional[torch.Tensor] = None,
-                       eps: float = 1e-6) -> Tuple[torch.Tensor, torch.Tensor]:
+                       eps: float = 1e-6, grad_slab=None) -> Tuple[torch.Tensor, torch.Tensor]:
         """q [T, H, D], k [T, H_KV, D]; position of token t = t - cu[seq(t)]
         (the HIP rotary kernel; GPU tensors only).  With norm weights the
-        rows are RMS-normalised first, in the same launch."""
-        return rope_varlen(q, k, cu_seqlens, self.inv_freq, norm_q, norm_k, eps)
+        rows are RMS-normalised first, in the same launch.  grad_slab: where
+        the backward writes dq, dk (GradSlab blocks 0 and 1)."""
+        return rope_varlen(q, k, cu_seqlens, self.inv_freq, norm_q, norm_k, eps, grad_slab)
 
 
 def _stacked_view(ws) -> Optional[torch.Tensor]:
@@ -215,6 +230,28 @@ def _stacked_view(ws) -> Optional[torch.Tensor]:
         off += w.numel()
     rows = sum(w.shape[0] for w in ws)
     return w0.detach().new_empty(0).set_(st, w0.storage_offset(), (rows, E), (E, 1))
+
+
+class GradSlab:
+    """One [rows, sum(sizes)] buffer whose consecutive column blocks receive
+    the gradients of the stacked projection's outputs (q, k, v, R_q, R_k),
+    written there by the kernels that produce them (the RoPE backward: dq,
+    dk; the attention backward: dv, dR_q, dR_k).  The projection's backward
+    then finds its cotangents as column blocks of one buffer and runs one dx
+    and one dW GEMM, with no concatenation.  Allocated by the first backward
+    that asks for a block; a block is a view of it with the gradient's
+    shape."""
+
+    def __init__(self, rows: int, sizes, dtype: torch.dtype, device):
+        self.rows, self.sizes, self.dtype, self.device = rows, list(sizes), dtype, device
+        self.buf = None
+
+    def block(self, i: int, shape) -> torch.Tensor:
+        if self.buf is None:
+            self.buf = torch.empty(self.rows, sum(self.sizes), dtype=self.dtype,
+                                   device=self.device)
+        c0 = sum(self.sizes[:i])
+        return self.buf[:, c0:c0 + self.sizes[i]].view(shape)
 
 
 def _column_blocks(gs, sizes) -> Optional[torch.Tensor]:
@@ -328,6 +365,11 @@ class NaylisAttention(nn.Module):
     with R_q, R_k low-rank projections of x for the first H_G = num_heads -
     vanilla_heads heads.  Constructor and forward as attention_fna2.py:197-215
     and :380-390."""
+
+    # The packed path's backward writes the gradients of q, k, v, R_q, R_k
+    # into one buffer (GradSlab); False: separate tensors (the same values up
+    # to the rounding of the projection's GEMMs).
+    _grad_slab = True
 
     def __init__(
         self,
@@ -689,13 +731,24 @@ class NaylisAttention(nn.Module):
         T = x.shape[0]
         scale = self._attn_scale()
         q, k, v, r_q, r_k = self._project(x)
+        # The backward's gradients of q, k, v, R_q, R_k as column blocks of
+        # one buffer (see GradSlab): where the RoPE launch and the attention
+        # kernels run eagerly on bf16 projections.
+        slab = None
+        if (self._grad_slab and torch.is_grad_enabled() and self.rope is not None and
+                self._use_fna2 and
+                q.dtype == torch.bfloat16 and type(q) is torch.Tensor and
+                _fna2_plain_eager(q)):
+            gr = self.graph_heads * self.rel_rank
+            slab = GradSlab(T, [self.embed_dim, self.kv_dim, self.kv_dim] + ([gr, gr] if gr else []),
+                            q.dtype, q.device)
         if self.rope is not None:  # QK-RMSNorm (if any) and RoPE in one launch
             assert not self.use_qk_norm or self.q_norm.eps == self.k_norm.eps
             q, k = self.rope.forward_varlen(
                 q, k, cu_seqlens_q,
                 self.q_norm.weight if self.use_qk_norm else None,
                 self.k_norm.weight if self.use_qk_norm else None,
-                self.q_norm.eps if self.use_qk_norm else 1e-6)
+                self.q_norm.eps if self.use_qk_norm else 1e-6, grad_slab=slab)
         elif self.use_qk_norm:
             q, k = self.q_norm(q), self.k_norm(k)
         orig_dtype = q.dtype
@@ -710,5 +763,5 @@ class NaylisAttention(nn.Module):
         gs = self.graph_scale.to(torch.float32) if self.graph_heads > 0 else None
         out = _flash_naylis_attn(q, k, v, r_q, r_k, gs, softmax_scale=scale, is_causal=True,
                                  cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_k,
-                                 max_seqlen_q=msq, max_seqlen_k=msk)
+                                 max_seqlen_q=msq, max_seqlen_k=msk, grad_slab=slab)
         return self._finish(out.reshape(T, self.embed_dim), orig_dtype), None

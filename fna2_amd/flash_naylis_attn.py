@@ -381,9 +381,12 @@ def _fna2_backward_varlen(
     softmax_scale: float,
     is_causal: bool = True,
     plan: Optional[torch.Tensor] = None,
+    grads_out: Optional[tuple] = None,
 ) -> tuple:
     """Varlen backward; returns (dq, dk, dv, dr_q, dr_k, d_gs).  Mirrors :1215-1300.
-    ``plan``: the one the forward of the same problem filled (optional)."""
+    ``plan``: the one the forward of the same problem filled (optional).
+    ``grads_out``: (dq, dk, dv, dr_q, dr_k) tensors to write the gradients
+    into, None entries allocated here (any row strides, unit last stride)."""
     total_q, H, D = q.shape
     total_k, H_KV = k.shape[0], k.shape[1]
     H_G = 0 if r_q is None else r_q.shape[1]
@@ -398,7 +401,10 @@ def _fna2_backward_varlen(
     # row-major [T, H] alike)
     # [T, H] view of head-major memory: the dK/dV kernel reads a head's rows
     delta = torch.empty(H, total_q, device=q.device, dtype=torch.float32).t()
-    dq, dk, dv, dr_q, dr_k = _grads_like(q, k, v, r_q, r_k, H_G)
+    grads = _grads_like(q, k, v, r_q, r_k, H_G)
+    if grads_out is not None:
+        grads = tuple(g if o is None else o for g, o in zip(grads, grads_out))
+    dq, dk, dv, dr_q, dr_k = grads
     d_gs = torch.empty(max(H_G, 1), device=q.device, dtype=torch.float32)
     prob = _problem(True, N, max_seqlen_q, max_seqlen_k, total_q, total_k, H, H_KV, H_G, D, R,
                     is_causal, softmax_scale, cu_q, cu_k, dtype=q.dtype)
@@ -475,6 +481,7 @@ class FlashNaylisAttnFunc(torch.autograd.Function):
         cu_seqlens_k=None,
         max_seqlen_q: int = 0,
         max_seqlen_k: int = 0,
+        grad_slab=None,
     ):
         use_varlen = cu_seqlens_q is not None
         if use_varlen:
@@ -502,16 +509,25 @@ class FlashNaylisAttnFunc(torch.autograd.Function):
         ctx.cu_seqlens_k = cu_seqlens_k
         ctx.max_seqlen_q = max_seqlen_q
         ctx.max_seqlen_k = max_seqlen_k
+        # (varlen) where the caller wants dv, dr_q and dr_k written: blocks
+        # 2, 3, 4 of a GradSlab (attention_fna2.py); None: new tensors
+        ctx.grad_slab = grad_slab if use_varlen else None
         return out
 
     @staticmethod
     def backward(ctx, dout):
         q, k, v, r_q, r_k, graph_scale, out, lse = ctx.saved_tensors
         if ctx.use_varlen:
+            slab = ctx.grad_slab
+            outs = None
+            if slab is not None:
+                outs = (None, None, slab.block(2, v.shape),
+                        None if r_q is None else slab.block(3, r_q.shape),
+                        None if r_k is None else slab.block(4, r_k.shape))
             grads = _fna2_backward_varlen(
                 dout, q, k, v, r_q, r_k, graph_scale, out, lse,
                 ctx.cu_seqlens_q, ctx.cu_seqlens_k, ctx.max_seqlen_q, ctx.max_seqlen_k,
-                ctx.softmax_scale, ctx.is_causal, plan=ctx.plan,
+                ctx.softmax_scale, ctx.is_causal, plan=ctx.plan, grads_out=outs,
             )
         else:
             grads = _fna2_backward(
@@ -519,7 +535,7 @@ class FlashNaylisAttnFunc(torch.autograd.Function):
                 ctx.softmax_scale, ctx.is_causal,
             )
         dq, dk, dv, dr_q, dr_k, d_gs = grads
-        return dq, dk, dv, dr_q, dr_k, d_gs, None, None, None, None, None, None
+        return dq, dk, dv, dr_q, dr_k, d_gs, None, None, None, None, None, None, None
 
 
 # ─────────────────────────────────────────────────────────────────────────────

@@ -100,9 +100,11 @@ def rope_varlen_raw(q: torch.Tensor, k: torch.Tensor, cu_seqlens: torch.Tensor,
 
 
 def rope_varlen_bwd(dq_out, dk_out, q, k, cu_seqlens, inv_freq, sign=1, norm_q=None,
-                    norm_k=None, eps=1e-6):
+                    norm_k=None, eps=1e-6, dq=None, dk=None):
     """Gradients (dq, dk, dnorm_q, dnorm_k) of ``rope_varlen_raw`` for the
-    gradients of its outputs (q, k: its inputs, needed with a norm)."""
+    gradients of its outputs (q, k: its inputs, needed with a norm).  dq, dk:
+    tensors of q's and k's shapes to write into (any row strides, unit last
+    stride), else new ones."""
     q, k = _usable(q), _usable(k)
     dq_out, dk_out = _usable(dq_out.to(q.dtype)), _usable(dk_out.to(k.dtype))
     cu = cu_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
@@ -110,8 +112,10 @@ def rope_varlen_bwd(dq_out, dk_out, q, k, cu_seqlens, inv_freq, sign=1, norm_q=N
     wq, wk = _f32(norm_q, q.device), _f32(norm_k, q.device)
     b = _capi.RopeBwdArgs()
     b.fwd = _args(q, k, cu, inv, sign, wq, wk, eps)
-    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
-    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+    if dq is None:
+        dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+    if dk is None:
+        dk = torch.empty_like(k, memory_format=torch.contiguous_format)
     b.dq_out, b.dk_out, b.dq, b.dk = _view(dq_out), _view(dk_out), _view(dq), _view(dk)
     dwq = None if wq is None else torch.empty_like(wq)
     dwk = None if wk is None else torch.empty_like(wk)
@@ -130,8 +134,9 @@ class RopeVarlenFunc(torch.autograd.Function):
     """y = R(angle) RMSNorm(x) (norm optional) on q and k."""
 
     @staticmethod
-    def forward(ctx, q, k, cu_seqlens, inv_freq, norm_q, norm_k, eps):
+    def forward(ctx, q, k, cu_seqlens, inv_freq, norm_q, norm_k, eps, grad_slab=None):
         ctx.eps = eps
+        ctx.grad_slab = grad_slab  # dq, dk into its blocks 0 and 1 (attention_fna2.py)
         ctx.norm = norm_q is not None or norm_k is not None
         ctx.save_for_backward(q if ctx.norm else None, k if ctx.norm else None,
                               cu_seqlens, inv_freq, norm_q, norm_k)
@@ -144,19 +149,22 @@ class RopeVarlenFunc(torch.autograd.Function):
         q, k, cu, inv, wq, wk = ctx.saved_tensors
         if not ctx.norm:  # the inverse rotation reads no inputs: any same-shaped tensors do
             q, k = dq, dk
-        gq, gk, gwq, gwk = rope_varlen_bwd(dq, dk, q, k, cu, inv, 1, wq, wk, ctx.eps)
+        slab = ctx.grad_slab
+        oq = None if slab is None else slab.block(0, ctx.shapes[0])
+        ok = None if slab is None else slab.block(1, ctx.shapes[1])
+        gq, gk, gwq, gwk = rope_varlen_bwd(dq, dk, q, k, cu, inv, 1, wq, wk, ctx.eps, oq, ok)
         if gwq is not None and wq is not None:
             gwq = gwq.to(wq.dtype)
         if gwk is not None and wk is not None:
             gwk = gwk.to(wk.dtype)
-        return gq, gk, None, None, gwq, gwk, None
+        return gq, gk, None, None, gwq, gwk, None, None
 
 
 def rope_varlen(q: torch.Tensor, k: torch.Tensor, cu_seqlens: torch.Tensor,
                 inv_freq: torch.Tensor, norm_q: Optional[torch.Tensor] = None,
-                norm_k: Optional[torch.Tensor] = None, eps: float = 1e-6
+                norm_k: Optional[torch.Tensor] = None, eps: float = 1e-6, grad_slab=None
                 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Varlen RoPE of q ``[T, H, D]`` and k ``[T, H_KV, D]``, optionally
     after the QK RMSNorm with weights ``norm_q`` / ``norm_k`` (differentiable
-    in q, k and the weights)."""
-    return RopeVarlenFunc.apply(q, k, cu_seqlens, inv_freq, norm_q, norm_k, eps)
+    in q, k and the weights).  grad_slab: see attention_fna2.GradSlab."""
+    return RopeVarlenFunc.apply(q, k, cu_seqlens, inv_freq, norm_q, norm_k, eps, grad_slab)

@@ -458,6 +458,57 @@ def test_module_varlen_bf16_attention_against_oracle(gpu, monkeypatch):
         assert w.grad is not None and torch.isfinite(w.grad.float()).all()
 
 
+@pytest.mark.gpu
+def test_module_varlen_gradient_slab(gpu, monkeypatch):
+    """The packed bf16 path hands the projection's backward its five
+    cotangents as column blocks of one buffer (written there by the RoPE and
+    attention backward kernels), so that it runs one dx and one dW GEMM; the
+    gradients of x and of every parameter equal those of the path with
+    separate gradient tensors (bf16 GEMM rounding apart)."""
+    import numpy as np
+    torch.manual_seed(12)
+    lens = [37, 200, 1, 90, 128]
+    T = sum(lens)
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32, device=gpu)
+    x0 = torch.randn(T, 512, device=gpu, dtype=torch.bfloat16)
+    g = torch.randn(T, 512, device=gpu, dtype=torch.bfloat16)
+    seen = []
+    real = A._column_blocks
+
+    def recording(gs, sizes):
+        r = real(gs, sizes)
+        seen.append(r is not None)
+        return r
+
+    monkeypatch.setattr(A, "_column_blocks", recording)
+
+    def run(slab):
+        monkeypatch.setattr(A.NaylisAttention, "_grad_slab", slab)
+        torch.manual_seed(3)
+        m = A.NaylisAttention(512, 4, n_kv_heads=2, rel_rank=32, vanilla_heads=1).to(
+            device=gpu, dtype=torch.bfloat16)
+        m._use_fna2 = True
+        with torch.no_grad():
+            m.graph_scale.uniform_(0.5, 1.5)
+        x = x0.clone().requires_grad_(True)
+        y, _ = m(x, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=200, max_seqlen_k=200)
+        y.backward(g)
+        torch.cuda.synchronize()
+        return [x.grad] + [p.grad for _, p in m.named_parameters()]
+
+    seen.clear()
+    with_slab = run(True)
+    assert seen and all(seen), seen  # one buffer: the one-GEMM backward ran
+    seen.clear()
+    without = run(False)
+    assert seen and not any(seen), seen
+    for a, b in zip(with_slab, without):
+        assert (a is None) == (b is None)
+        if a is not None:
+            rel = ((a.float() - b.float()).norm() / b.float().norm().clamp_min(1e-6)).item()
+            assert rel < 2e-2, rel
+
+
 def test_stacked_projection_gradient_paths_agree():
     """Backward of the one-GEMM projection: incoming gradients that are
     consecutive column blocks of one buffer take one dx GEMM; separate ones
