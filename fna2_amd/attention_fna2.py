@@ -240,16 +240,21 @@ class GradSlab:
     then finds its cotangents as column blocks of one buffer and runs one dx
     and one dW GEMM, with no concatenation.  Allocated by the first backward
     that asks for a block; a block is a view of it with the gradient's
-    shape."""
+    shape.  A block asked for again (a second backward through a retained
+    graph) starts a new buffer, so that gradients already returned are never
+    overwritten."""
 
     def __init__(self, rows: int, sizes, dtype: torch.dtype, device):
         self.rows, self.sizes, self.dtype, self.device = rows, list(sizes), dtype, device
         self.buf = None
+        self.given = set()
 
     def block(self, i: int, shape) -> torch.Tensor:
-        if self.buf is None:
+        if self.buf is None or i in self.given:
             self.buf = torch.empty(self.rows, sum(self.sizes), dtype=self.dtype,
                                    device=self.device)
+            self.given = set()
+        self.given.add(i)
         c0 = sum(self.sizes[:i])
         return self.buf[:, c0:c0 + self.sizes[i]].view(shape)
 

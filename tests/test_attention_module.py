@@ -509,6 +509,23 @@ def test_module_varlen_gradient_slab(gpu, monkeypatch):
             assert rel < 2e-2, rel
 
 
+def test_grad_slab_blocks_and_second_pass():
+    """GradSlab blocks are column views of one buffer; asking for a block
+    again (a second backward) starts a new buffer, leaving the views already
+    handed out untouched."""
+    s = A.GradSlab(5, [8, 4, 4], torch.float32, "cpu")
+    a0, a1 = s.block(0, (5, 2, 4)), s.block(2, (5, 4))
+    assert a0.untyped_storage().data_ptr() == a1.untyped_storage().data_ptr()
+    assert a1.storage_offset() - a0.storage_offset() == 12 and a0.stride(0) == 16
+    a0.fill_(1.0)
+    b0 = s.block(0, (5, 2, 4))  # a second pass
+    assert b0.untyped_storage().data_ptr() != a0.untyped_storage().data_ptr()
+    b0.fill_(2.0)
+    assert torch.all(a0 == 1.0)
+    blocks = [s.block(1, (5, 4)), s.block(2, (5, 4))]
+    assert A._column_blocks([b0.view(5, 8)] + blocks, [8, 4, 4]) is not None
+
+
 def test_stacked_projection_gradient_paths_agree():
     """Backward of the one-GEMM projection: incoming gradients that are
     consecutive column blocks of one buffer take one dx GEMM; separate ones
