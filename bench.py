@@ -591,7 +591,9 @@ def module_bench(args):
     the norm + RoPE launch, the attention kernels and the output projection.
     ``value``: with the projection's gradients written into one buffer
     (GradSlab: one dx and one dW GEMM); ``separate_ms``: with separate
-    gradient tensors."""
+    gradient tensors; ``dense_ms``: a dense layer of c2's geometry ([4, 2048,
+    1024] input, 16 heads of 64, 16 graph heads of rank 16), forward +
+    backward, whose QK-norm and RoPE run in the same launch."""
     import numpy as np
     import torch
 
@@ -617,6 +619,17 @@ def module_bench(args):
                  max_seqlen_k=max(lens))
         y.backward(g)
 
+    torch.manual_seed(0)
+    md = A.NaylisAttention(1024, 16, rel_rank=16, max_seq_len=2048).to(device=dev,
+                                                                       dtype=torch.bfloat16)
+    md._use_fna2 = True
+    xd = torch.randn(4, 2048, 1024, device=dev, dtype=torch.bfloat16, requires_grad=True)
+    gd = torch.randn(4, 2048, 1024, device=dev, dtype=torch.bfloat16)
+
+    def dense_step():
+        y, _ = md(xd)
+        y.backward(gd)
+
     res = {}
     try:
         for slab in (True, False):
@@ -633,6 +646,16 @@ def module_bench(args):
             res[slab] = e0.elapsed_time(e1) / args.steps
     finally:
         A.NaylisAttention._grad_slab = True
+    for _ in range(max(args.warmup, 10)):
+        dense_step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        dense_step()
+    e1.record()
+    torch.cuda.synchronize()
+    res["dense"] = e0.elapsed_time(e1) / args.steps
     print(json.dumps({
         "metric": "NaylisAttention packed layer fwd+bwd tokens/s (c3 pack, E=2048)",
         "value": round(T / (res[True] * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
@@ -643,6 +666,8 @@ def module_bench(args):
                                f"{len(lens)} seqs, QK-RMSNorm + RoPE, causal"},
         "separate_grads_ms": round(res[False], 4),
         "speedup_over_separate_grads": round(res[False] / res[True], 3),
+        "dense_ms": round(res["dense"], 4),
+        "dense_workload": "NaylisAttention(1024, 16, rel_rank=16) on [4, 2048, 1024], causal",
     }), flush=True)
 
 

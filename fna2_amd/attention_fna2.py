@@ -70,8 +70,9 @@ def _attention(q, k, v, r_q, r_k, graph_scale, grad_slab=None, **kw):
     if grad_slab is None:
         return flash_naylis_attn(q, k, v, r_q, r_k, graph_scale, **kw)
     return _FNA2Func.apply(q, k, v, r_q, r_k, graph_scale, float(kw["softmax_scale"]),
-                           bool(kw["is_causal"]), kw["cu_seqlens_q"], kw["cu_seqlens_k"],
-                           int(kw["max_seqlen_q"]), int(kw["max_seqlen_k"]), grad_slab)
+                           bool(kw["is_causal"]), kw.get("cu_seqlens_q"), kw.get("cu_seqlens_k"),
+                           int(kw.get("max_seqlen_q", 0)), int(kw.get("max_seqlen_k", 0)),
+                           grad_slab)
 
 
 _flash_naylis_attn = _attention
@@ -249,14 +250,19 @@ class GradSlab:
         self.buf = None
         self.given = set()
 
-    def block(self, i: int, shape) -> torch.Tensor:
+    def block(self, i: int, like) -> torch.Tensor:
+        """The gradient of output block i in the layout of ``like``: a view
+        of column block i of the projection's output (its strides are in
+        that output's [rows, sum(sizes)] geometry, which the buffer has too),
+        or a (shape, strides) pair of such a view."""
         if self.buf is None or i in self.given:
             self.buf = torch.empty(self.rows, sum(self.sizes), dtype=self.dtype,
                                    device=self.device)
             self.given = set()
         self.given.add(i)
+        shape, stride = (like.shape, like.stride()) if torch.is_tensor(like) else like
         c0 = sum(self.sizes[:i])
-        return self.buf[:, c0:c0 + self.sizes[i]].view(shape)
+        return self.buf.as_strided(shape, stride, self.buf.storage_offset() + c0)
 
 
 def _column_blocks(gs, sizes) -> Optional[torch.Tensor]:
@@ -581,11 +587,28 @@ class NaylisAttention(nn.Module):
             v = self.v_proj(x).view(B, S, self.n_kv_heads, self.head_dim).transpose(1, 2)
             if keep_rk:
                 r_q, r_k = self._rel(x)
-        if self.use_qk_norm:
-            q, k = self.q_norm(q), self.k_norm(k)
+        slab = None
         offset = past_kv[0].shape[2] if past_kv is not None else 0
-        if self.rope is not None:
-            q, k = self.rope(q, k, position_offset=offset)
+        if fused and self.rope is not None:
+            # QK-RMSNorm and RoPE in the varlen launch: the batch's rows are B
+            # sequences of S tokens (positions 0 .. S - 1), read where the
+            # projection wrote them
+            assert not self.use_qk_norm or self.q_norm.eps == self.k_norm.eps
+            slab = self._slab_for(q, B * S)
+            qf = q.transpose(1, 2).reshape(B * S, self.num_heads, self.head_dim)
+            kf = k.transpose(1, 2).reshape(B * S, self.n_kv_heads, self.head_dim)
+            qr, kr = self.rope.forward_varlen(
+                qf, kf, self._batch_cu(B, S, x.device),
+                self.q_norm.weight if self.use_qk_norm else None,
+                self.k_norm.weight if self.use_qk_norm else None,
+                self.q_norm.eps if self.use_qk_norm else 1e-6, grad_slab=slab)
+            q = qr.view(B, S, self.num_heads, self.head_dim).transpose(1, 2)
+            k = kr.view(B, S, self.n_kv_heads, self.head_dim).transpose(1, 2)
+        else:
+            if self.use_qk_norm:
+                q, k = self.q_norm(q), self.k_norm(k)
+            if self.rope is not None:
+                q, k = self.rope(q, k, position_offset=offset)
         if past_kv is not None:
             k = torch.cat([past_kv[0], k], dim=2)
             v = torch.cat([past_kv[1], v], dim=2)
@@ -604,7 +627,7 @@ class NaylisAttention(nn.Module):
 
         if fused:
             out = _flash_naylis_attn(q, k, v, r_q, r_k, self.graph_scale.to(torch.float32),
-                                     softmax_scale=scale, is_causal=is_causal)
+                                     softmax_scale=scale, is_causal=is_causal, grad_slab=slab)
         elif kernel_decode:
             out = flash_naylis_decode(
                 q, k, v, r_q if cached_bias else None, r_k if cached_bias else None,
@@ -731,6 +754,25 @@ class NaylisAttention(nn.Module):
             w = self.dropout(w)
         return torch.matmul(w, v)
 
+    def _slab_for(self, q: torch.Tensor, rows: int) -> Optional[GradSlab]:
+        """A GradSlab for this call's projection gradients, where the RoPE
+        launch and the attention op run eagerly on its bf16 outputs."""
+        if not (self._grad_slab and torch.is_grad_enabled() and self._use_fna2 and
+                q.dtype == torch.bfloat16 and type(q) is torch.Tensor and
+                _fna2_plain_eager(q)):
+            return None
+        gr = self.graph_heads * self.rel_rank
+        return GradSlab(rows, [self.embed_dim, self.kv_dim, self.kv_dim] + ([gr, gr] if gr else []),
+                        q.dtype, q.device)
+
+    def _batch_cu(self, B: int, S: int, device) -> torch.Tensor:
+        """cu_seqlens of B sequences of S tokens (kept for the next call)."""
+        key = (B, S, device)
+        if getattr(self, "_cu_key", None) != key:
+            self._cu = torch.arange(0, B * S + 1, S, dtype=torch.int32, device=device)
+            self._cu_key = key
+        return self._cu
+
     def _forward_varlen(self, x, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k):
         """x [T, E] packed (attention_fna2.py:533-617); causal within each sequence."""
         T = x.shape[0]
@@ -739,14 +781,7 @@ class NaylisAttention(nn.Module):
         # The backward's gradients of q, k, v, R_q, R_k as column blocks of
         # one buffer (see GradSlab): where the RoPE launch and the attention
         # kernels run eagerly on bf16 projections.
-        slab = None
-        if (self._grad_slab and torch.is_grad_enabled() and self.rope is not None and
-                self._use_fna2 and
-                q.dtype == torch.bfloat16 and type(q) is torch.Tensor and
-                _fna2_plain_eager(q)):
-            gr = self.graph_heads * self.rel_rank
-            slab = GradSlab(T, [self.embed_dim, self.kv_dim, self.kv_dim] + ([gr, gr] if gr else []),
-                            q.dtype, q.device)
+        slab = self._slab_for(q, T) if self.rope is not None else None
         if self.rope is not None:  # QK-RMSNorm (if any) and RoPE in one launch
             assert not self.use_qk_norm or self.q_norm.eps == self.k_norm.eps
             q, k = self.rope.forward_varlen(

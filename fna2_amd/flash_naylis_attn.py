@@ -350,8 +350,10 @@ def _fna2_backward(
     out, lse,
     softmax_scale: float,
     is_causal: bool,
+    grads_out: Optional[tuple] = None,
 ) -> tuple:
-    """Dense backward; returns (dq, dk, dv, dr_q, dr_k, d_gs).  Mirrors :807-892."""
+    """Dense backward; returns (dq, dk, dv, dr_q, dr_k, d_gs).  Mirrors :807-892.
+    ``grads_out``: as for ``_fna2_backward_varlen``."""
     B, H, S, D = q.shape
     H_KV, S_k = k.shape[1], k.shape[2]
     H_G = 0 if r_q is None else r_q.shape[1]
@@ -361,7 +363,10 @@ def _fna2_backward(
     gs = _gs32(graph_scale) if H_G else None
     lse = lse.contiguous()
     delta = torch.empty(B, H, S, device=q.device, dtype=torch.float32)
-    dq, dk, dv, dr_q, dr_k = _grads_like(q, k, v, r_q, r_k, H_G)
+    grads = _grads_like(q, k, v, r_q, r_k, H_G)
+    if grads_out is not None:
+        grads = tuple(g if o is None else o for g, o in zip(grads, grads_out))
+    dq, dk, dv, dr_q, dr_k = grads
     d_gs = torch.empty(max(H_G, 1), device=q.device, dtype=torch.float32)
     prob = _problem(False, B, S, S_k, 0, 0, H, H_KV, H_G, D, R, is_causal, softmax_scale,
                     dtype=q.dtype)
@@ -509,21 +514,21 @@ class FlashNaylisAttnFunc(torch.autograd.Function):
         ctx.cu_seqlens_k = cu_seqlens_k
         ctx.max_seqlen_q = max_seqlen_q
         ctx.max_seqlen_k = max_seqlen_k
-        # (varlen) where the caller wants dv, dr_q and dr_k written: blocks
-        # 2, 3, 4 of a GradSlab (attention_fna2.py); None: new tensors
-        ctx.grad_slab = grad_slab if use_varlen else None
+        # where the caller wants dv, dr_q and dr_k written: blocks 2, 3, 4 of
+        # a GradSlab (attention_fna2.py); None: new tensors
+        ctx.grad_slab = grad_slab
         return out
 
     @staticmethod
     def backward(ctx, dout):
         q, k, v, r_q, r_k, graph_scale, out, lse = ctx.saved_tensors
+        slab = ctx.grad_slab
+        outs = None
+        if slab is not None:
+            outs = (None, None, slab.block(2, v),
+                    None if r_q is None else slab.block(3, r_q),
+                    None if r_k is None else slab.block(4, r_k))
         if ctx.use_varlen:
-            slab = ctx.grad_slab
-            outs = None
-            if slab is not None:
-                outs = (None, None, slab.block(2, v.shape),
-                        None if r_q is None else slab.block(3, r_q.shape),
-                        None if r_k is None else slab.block(4, r_k.shape))
             grads = _fna2_backward_varlen(
                 dout, q, k, v, r_q, r_k, graph_scale, out, lse,
                 ctx.cu_seqlens_q, ctx.cu_seqlens_k, ctx.max_seqlen_q, ctx.max_seqlen_k,
@@ -532,7 +537,7 @@ class FlashNaylisAttnFunc(torch.autograd.Function):
         else:
             grads = _fna2_backward(
                 dout, q, k, v, r_q, r_k, graph_scale, out, lse,
-                ctx.softmax_scale, ctx.is_causal,
+                ctx.softmax_scale, ctx.is_causal, grads_out=outs,
             )
         dq, dk, dv, dr_q, dr_k, d_gs = grads
         return dq, dk, dv, dr_q, dr_k, d_gs, None, None, None, None, None, None, None

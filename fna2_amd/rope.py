@@ -141,6 +141,8 @@ class RopeVarlenFunc(torch.autograd.Function):
         ctx.save_for_backward(q if ctx.norm else None, k if ctx.norm else None,
                               cu_seqlens, inv_freq, norm_q, norm_k)
         ctx.shapes = (q.shape, k.shape)
+        # the layouts the gradients take in a GradSlab (as q's and k's)
+        ctx.layouts = ((q.shape, q.stride()), (k.shape, k.stride()))
         return rope_varlen_raw(q, k, cu_seqlens, inv_freq, 1, norm_q, norm_k, eps)
 
     @staticmethod
@@ -150,8 +152,8 @@ class RopeVarlenFunc(torch.autograd.Function):
         if not ctx.norm:  # the inverse rotation reads no inputs: any same-shaped tensors do
             q, k = dq, dk
         slab = ctx.grad_slab
-        oq = None if slab is None else slab.block(0, ctx.shapes[0])
-        ok = None if slab is None else slab.block(1, ctx.shapes[1])
+        oq = None if slab is None else slab.block(0, ctx.layouts[0])
+        ok = None if slab is None else slab.block(1, ctx.layouts[1])
         gq, gk, gwq, gwk = rope_varlen_bwd(dq, dk, q, k, cu, inv, 1, wq, wk, ctx.eps, oq, ok)
         if gwq is not None and wq is not None:
             gwq = gwq.to(wq.dtype)

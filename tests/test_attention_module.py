@@ -459,19 +459,22 @@ def test_module_varlen_bf16_attention_against_oracle(gpu, monkeypatch):
 
 
 @pytest.mark.gpu
-def test_module_varlen_gradient_slab(gpu, monkeypatch):
-    """The packed bf16 path hands the projection's backward its five
-    cotangents as column blocks of one buffer (written there by the RoPE and
-    attention backward kernels), so that it runs one dx and one dW GEMM; the
-    gradients of x and of every parameter equal those of the path with
-    separate gradient tensors (bf16 GEMM rounding apart)."""
+@pytest.mark.parametrize("packed", [True, False])
+def test_module_gradient_slab(gpu, monkeypatch, packed):
+    """The bf16 FNA2 paths (packed, and dense [B, S, E], whose QK-norm and
+    RoPE also run in the varlen launch) hand the projection's backward its
+    five cotangents as column blocks of one buffer (written there by the
+    RoPE and attention backward kernels), so that it runs one dx and one dW
+    GEMM; the gradients of x and of every parameter equal those of the path
+    with separate gradient tensors (bf16 GEMM rounding apart)."""
     import numpy as np
     torch.manual_seed(12)
     lens = [37, 200, 1, 90, 128]
     T = sum(lens)
     cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32, device=gpu)
-    x0 = torch.randn(T, 512, device=gpu, dtype=torch.bfloat16)
-    g = torch.randn(T, 512, device=gpu, dtype=torch.bfloat16)
+    shape = (T, 512) if packed else (3, 150, 512)
+    x0 = torch.randn(*shape, device=gpu, dtype=torch.bfloat16)
+    g = torch.randn(*shape, device=gpu, dtype=torch.bfloat16)
     seen = []
     real = A._column_blocks
 
@@ -491,7 +494,10 @@ def test_module_varlen_gradient_slab(gpu, monkeypatch):
         with torch.no_grad():
             m.graph_scale.uniform_(0.5, 1.5)
         x = x0.clone().requires_grad_(True)
-        y, _ = m(x, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=200, max_seqlen_k=200)
+        if packed:
+            y, _ = m(x, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=200, max_seqlen_k=200)
+        else:
+            y, _ = m(x)
         y.backward(g)
         torch.cuda.synchronize()
         return [x.grad] + [p.grad for _, p in m.named_parameters()]
@@ -514,16 +520,25 @@ def test_grad_slab_blocks_and_second_pass():
     again (a second backward) starts a new buffer, leaving the views already
     handed out untouched."""
     s = A.GradSlab(5, [8, 4, 4], torch.float32, "cpu")
-    a0, a1 = s.block(0, (5, 2, 4)), s.block(2, (5, 4))
+    y = torch.zeros(5, 16)  # the projection's output geometry
+    q, v = y[:, :8].view(5, 2, 4), y[:, 12:]
+    a0, a1 = s.block(0, q), s.block(2, v)
+    assert a0.shape == q.shape and a0.stride() == q.stride() and a1.stride() == v.stride()
     assert a0.untyped_storage().data_ptr() == a1.untyped_storage().data_ptr()
-    assert a1.storage_offset() - a0.storage_offset() == 12 and a0.stride(0) == 16
+    assert a1.storage_offset() - a0.storage_offset() == 12
     a0.fill_(1.0)
-    b0 = s.block(0, (5, 2, 4))  # a second pass
+    b0 = s.block(0, (q.shape, q.stride()))  # a second pass
     assert b0.untyped_storage().data_ptr() != a0.untyped_storage().data_ptr()
     b0.fill_(2.0)
     assert torch.all(a0 == 1.0)
-    blocks = [s.block(1, (5, 4)), s.block(2, (5, 4))]
+    blocks = [s.block(1, y[:, 8:12]), s.block(2, v)]
     assert A._column_blocks([b0.view(5, 8)] + blocks, [8, 4, 4]) is not None
+    # a transposed [B, H, S, D] view (the dense path) keeps its strides
+    yd = torch.zeros(2, 3, 16)  # B = 2, S = 3
+    kd = yd[..., 8:12].view(2, 3, 2, 2).transpose(1, 2)
+    sd = A.GradSlab(6, [8, 4, 4], torch.float32, "cpu")
+    gk = sd.block(1, kd)
+    assert gk.shape == kd.shape and gk.stride() == kd.stride()
 
 
 def test_stacked_projection_gradient_paths_agree():
