@@ -615,6 +615,11 @@ def module_bench(args):
     g = torch.randn(T, E, device=dev, dtype=torch.bfloat16)
 
     def step():
+        # gradients set to None first, as a training step's zero_grad does
+        # (else every backward adds into the previous step's)
+        x.grad = None
+        for p_ in m.parameters():
+            p_.grad = None
         y, _ = m(x, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=max(lens),
                  max_seqlen_k=max(lens))
         y.backward(g)
@@ -627,6 +632,9 @@ def module_bench(args):
     gd = torch.randn(4, 2048, 1024, device=dev, dtype=torch.bfloat16)
 
     def dense_step():
+        xd.grad = None
+        for p_ in md.parameters():
+            p_.grad = None
         y, _ = md(xd)
         y.backward(gd)
 
