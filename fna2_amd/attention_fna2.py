@@ -254,15 +254,41 @@ class GradSlab:
         """The gradient of output block i in the layout of ``like``: a view
         of column block i of the projection's output (its strides are in
         that output's [rows, sum(sizes)] geometry, which the buffer has too),
-        or a (shape, strides) pair of such a view."""
+        or a (shape, strides) pair of such a view.  Any other layout gets a
+        tensor of its own (so the projection's backward takes its per-block
+        path)."""
+        shape, stride = (like.shape, like.stride()) if torch.is_tensor(like) else like
+        if not _block_layout(shape, stride, self.sizes[i], sum(self.sizes), self.rows):
+            return torch.empty(shape, dtype=self.dtype, device=self.device)
         if self.buf is None or i in self.given:
             self.buf = torch.empty(self.rows, sum(self.sizes), dtype=self.dtype,
                                    device=self.device)
             self.given = set()
         self.given.add(i)
-        shape, stride = (like.shape, like.stride()) if torch.is_tensor(like) else like
         c0 = sum(self.sizes[:i])
         return self.buf.as_strided(shape, stride, self.buf.storage_offset() + c0)
+
+
+def _block_layout(shape, stride, n: int, width: int, rows: int) -> bool:
+    """Whether (shape, stride) addresses exactly the first n columns of each
+    of ``rows`` rows of a row-major [rows, width] matrix: the dimensions of
+    stride below ``width`` tile the n columns densely, the others step whole
+    rows."""
+    inner = sorted((st, sz) for st, sz in zip(stride, shape) if st < width and sz > 1)
+    outer = [(st, sz) for st, sz in zip(stride, shape) if st >= width and sz > 1]
+    span = 1
+    for st, sz in inner:
+        if st != span:
+            return False
+        span *= sz
+    if span != n:
+        return False
+    last = 0
+    for st, sz in outer:
+        if st % width:
+            return False
+        last += (st // width) * (sz - 1)
+    return last < rows and math.prod(sz for _, sz in outer) == rows
 
 
 def _column_blocks(gs, sizes) -> Optional[torch.Tensor]:

@@ -539,6 +539,13 @@ def test_grad_slab_blocks_and_second_pass():
     sd = A.GradSlab(6, [8, 4, 4], torch.float32, "cpu")
     gk = sd.block(1, kd)
     assert gk.shape == kd.shape and gk.stride() == kd.stride()
+    # a layout that is not a column block (here a contiguous tensor, which
+    # would spill into the next blocks) gets a tensor of its own
+    c = torch.zeros(6, 2, 2)
+    gc = sd.block(1, c)
+    assert gc.untyped_storage().data_ptr() != gk.untyped_storage().data_ptr()
+    assert A._block_layout(kd.shape, kd.stride(), 4, 16, 6)
+    assert not A._block_layout(c.shape, c.stride(), 4, 16, 6)
 
 
 def test_stacked_projection_gradient_paths_agree():
