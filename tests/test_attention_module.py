@@ -152,6 +152,10 @@ def _pair(**kw):
 @pytest.mark.parametrize("kw", [
     dict(embed_dim=512, num_heads=8, rel_rank=32),
     dict(embed_dim=512, num_heads=4, n_kv_heads=2, rel_rank=16, vanilla_heads=1),
+    # YaRN-stretched frequencies and scale, and no QK-norm, through the fused launch
+    dict(embed_dim=512, num_heads=4, rel_rank=8, use_yarn=True, yarn_scale=4.0,
+         max_seq_len=256, yarn_original_max_len=64),
+    dict(embed_dim=512, num_heads=4, rel_rank=8, use_qk_norm=False),
 ])
 def test_fna2_path_matches_eager_dense(gpu, kw):
     assert A._FNA2_AVAILABLE
