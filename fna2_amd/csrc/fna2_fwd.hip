@@ -40,6 +40,12 @@ struct FwdCfg {
   static constexpr int RBYTES = BN * RPL * 2;
   static constexpr int VBYTES = BN * D * 2;
   static constexpr int STAGE = KBYTES + RBYTES + VBYTES;
+  // d = 128, rank tile <= 32: K operand reads in flight ahead of the S
+  // MFMAs and V^T operands ahead of the O MFMAs (the register budget of
+  // three waves per SIMD leaves room for two each; none at rank 64).
+  static constexpr bool PIPE = D == 128 && RPL <= 32;
+  static constexpr int kAhead = 2;
+  static constexpr int kAhead2 = 2;
 };
 
 // S16 (R <= 16, rank tile 32): the rank chain accumulates b <Rq, Rk>
@@ -192,15 +198,35 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
 #pragma unroll
     for (int kb2 = 0; kb2 < C::BN / 32; ++kb2) {
       f32x16 acc = f32x16{};
+      constexpr int A = C::PIPE ? C::kAhead : 1;
+      bf16x8 kr[A];
+      if constexpr (C::PIPE) {
+#pragma unroll
+        for (int s = 0; s < A; ++s) kr[s] = row_read<C::BN>(kl, rdl, kb2 * 32, s);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       if constexpr (C::KSR > 0) {
 #pragma unroll
         for (int s = 0; s < C::KSR; ++s)
           if (s < nrs) acc = mfma32(row_read<C::BN>(rl, rdl, kb2 * 32, s), qreg[C::KSD + s], acc);
         if constexpr (!S16) acc *= bh;
       }
+      if constexpr (C::PIPE) {
+        // the K operand reads A k-steps ahead of the MFMAs (issued before
+        // the rank chain; the scheduling fences keep every read where it is
+        // issued, else the compiler, short of registers, reads each operand
+        // just before its MFMA and waits for it)
 #pragma unroll
-      for (int s = 0; s < C::KSD; ++s)
-        acc = mfma_e<F16>(row_read<C::BN>(kl, rdl, kb2 * 32, s), qreg[s], acc);
+        for (int s = 0; s < C::KSD; ++s) {
+          acc = mfma_e<F16>(kr[s % A], qreg[s], acc);
+          if (s + A < C::KSD) kr[s % A] = row_read<C::BN>(kl, rdl, kb2 * 32, s + A);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < C::KSD; ++s)
+          acc = mfma_e<F16>(row_read<C::BN>(kl, rdl, kb2 * 32, s), qreg[s], acc);
+      }
       sacc[kb2] = acc;
     }
     if ((kbase + C::BN > e.lk) || (p.causal && kbase + C::BN - 1 > wq0)) {
@@ -253,11 +279,27 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
       }
     l_i += ls;
     // O^T += V^T P^T
+    if constexpr (C::PIPE) {
+      constexpr int A = C::kAhead2, N = (C::BN / 16) * (D / 32);
+      bf16x8 vr[A];
 #pragma unroll
-    for (int s = 0; s < C::BN / 16; ++s)
+      for (int i = 0; i < A; ++i) vr[i] = tr_operand<C::BN>(vl, tl, 16 * (i / (D / 32)), 32 * (i % (D / 32)));
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int d = 0; d < D / 32; ++d)
-        oacc[d] = mfma_e<F16>(tr_operand<C::BN>(vl, tl, 16 * s, 32 * d), pb[s], oacc[d]);
+      for (int i = 0; i < N; ++i) {
+        const int s = i / (D / 32), d = i % (D / 32);
+        oacc[d] = mfma_e<F16>(vr[i % A], pb[s], oacc[d]);
+        if (i + A < N)
+          vr[i % A] = tr_operand<C::BN>(vl, tl, 16 * ((i + A) / (D / 32)), 32 * ((i + A) % (D / 32)));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < C::BN / 16; ++s)
+#pragma unroll
+        for (int d = 0; d < D / 32; ++d)
+          oacc[d] = mfma_e<F16>(tr_operand<C::BN>(vl, tl, 16 * s, 32 * d), pb[s], oacc[d]);
+    }
   };
 
   for (int kt = 0; kt < nkv; kt += 2) {
