@@ -250,14 +250,22 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
     for (int kb2 = 0; kb2 < C::NKB; ++kb2) {
       f32x16 sacc = f32x16{}, dpacc = f32x16{};
       // At d = 128 the S and dP chains run interleaved, their K and V
-      // operand reads kAhead k-steps ahead of the MFMAs (issued before the
-      // rank chain; the scheduling fences keep every read where it is
-      // issued, else the compiler, short of registers, reads each operand
-      // just before its MFMA and waits for it).  c3 dQ -2.2 us, c4 -4%.
+      // operand reads kAhead k-steps ahead of the MFMAs, issued before the
+      // rank chain with (rank tile 32) that chain's Rk reads (read whether
+      // or not the head has a rank part; unused then).  The scheduling
+      // fences keep every read where it is issued, else the compiler, short
+      // of registers, reads each operand just before its MFMA and waits for
+      // it: c3 dQ 128.4 -> 123.3 us, c4 -4%.
       constexpr bool PIPE = D == 128;
       constexpr int A = PIPE ? C::kAhead : 1;
       bf16x8 kr[A], vr[A];
+      constexpr bool RPRE = PIPE && C::KSR > 0 && C::KSR <= 2;
+      bf16x8 rr[RPRE ? C::KSR : 1];
       if constexpr (PIPE) {
+        if constexpr (RPRE) {
+#pragma unroll
+          for (int s = 0; s < C::KSR; ++s) rr[s] = row_read<C::BN>(rt, rdl, kb2 * 32, s);
+        }
 #pragma unroll
         for (int s = 0; s < A; ++s) {
           kr[s] = row_read<C::BN>(kt, rdl, kb2 * 32, s);
@@ -270,7 +278,9 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
       if constexpr (C::KSR > 0) {
 #pragma unroll
         for (int s = 0; s < C::KSR; ++s)
-          if (s < nrs) sacc = mfma32(row_read<C::BN>(rt, rdl, kb2 * 32, s), qreg[C::KSD + s], sacc);
+          if (s < nrs)
+            sacc = mfma32(RPRE ? rr[RPRE ? s : 0] : row_read<C::BN>(rt, rdl, kb2 * 32, s),
+                          qreg[C::KSD + s], sacc);
         sacc *= bh;
       }
       if constexpr (PIPE) {
@@ -322,10 +332,17 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
       }
     }
     // dQa^T += Ka^T dA^T (at d = 128 the head-dim part first, its operand
-    // reads kAhead2 MFMAs ahead, then the rank part)
+    // reads kAhead2 MFMAs ahead, then the rank part, whose Rk^T operands
+    // (rank tile 32) are read with the first ones)
+    constexpr bool RPRE2 = C::NKB == 1 && D == 128 && C::NRB == 1;
+    bf16x8 rr2[2];
     if constexpr (C::NKB == 1 && D == 128) {
       constexpr int A = C::kAhead2, N = 2 * C::NDB;
       bf16x8 kr[A];
+      if constexpr (RPRE2) {
+        rr2[0] = tr_operand<C::BN>(rt, tl, 0, 0);
+        rr2[1] = tr_operand<C::BN>(rt, tl, 16, 0);
+      }
 #pragma unroll
       for (int i = 0; i < A; ++i) kr[i] = tr_operand<C::BN>(kt, tl, 16 * (i / C::NDB), 32 * (i % C::NDB));
       __builtin_amdgcn_sched_barrier(0);
@@ -352,7 +369,7 @@ __device__ __forceinline__ void dq_body(const BwdParams& P) {
           if (graph) {
 #pragma unroll
             for (int f = 0; f < C::NRB; ++f)
-              acc[C::NDB + f] = mfma32(tr_operand<C::BN>(rt, tl, k0, 32 * f),
+              acc[C::NDB + f] = mfma32(RPRE2 ? rr2[half] : tr_operand<C::BN>(rt, tl, k0, 32 * f),
                                        DBR ? dbr[DBR ? kb2 : 0][half] : db[kb2][half],
                                        acc[C::NDB + f]);
           }
