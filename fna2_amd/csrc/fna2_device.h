@@ -86,6 +86,15 @@ __device__ __forceinline__ float uni_f(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
 }
 
+// A wave-uniform float, opaque to the compiler where it is used: `acc *=
+// here_s(b)` for a 16-wide accumulator then multiplies by one scalar
+// register, instead of a splat of b that the compiler hoists out of the
+// loop and holds in 16 scalar registers (forcing other scalars to spill).
+__device__ __forceinline__ float here_s(float x) {
+  asm volatile("" : "+s"(x));
+  return x;
+}
+
 // Extents of sequence b (b may differ per lane).
 __device__ __forceinline__ SeqExt seq_ext(const Problem& p, int b) {
   SeqExt e;

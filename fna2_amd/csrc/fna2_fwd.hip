@@ -209,7 +209,7 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
 #pragma unroll
         for (int s = 0; s < C::KSR; ++s)
           if (s < nrs) acc = mfma32(row_read<C::BN>(rl, rdl, kb2 * 32, s), qreg[C::KSD + s], acc);
-        if constexpr (!S16) acc *= bh;
+        if constexpr (!S16) acc *= here_s(bh);
       }
       if constexpr (C::PIPE) {
         // the K operand reads A k-steps ahead of the MFMAs (issued before
