@@ -139,11 +139,22 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
     const uint32_t qxor = p.qa < 0.f ? 0x80008000u : 0u;
     const uint32_t qand = p.qa == 0.f ? 0u : 0xffffffffu;
 #pragma unroll
-    for (int s = 0; s < C::KSD; ++s) {
-      u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, vo + 32u * s, 0, 0);
+    for (int s = 0; s < C::KSD; ++s)
+      qreg[s] = as_bf16x8(__builtin_amdgcn_raw_buffer_load_b128(rs, vo + 32u * s, 0, 0));
+    // a Q (sign, or zero for a zero scale).  At d = 128 only where a != 1:
+    // the sign and mask need the loaded rows, and waiting for them holds
+    // the rank rows' loads below back by a round trip to memory (c3 forward
+    // -0.9 us, c4 -0.7%).  At d = 64 that wait measured faster (c2 +1.1 us
+    // without it: its single round of workgroups issues every row at once),
+    // and so it stays.
+    if (D == 64 || p.qa != 1.f) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = (v[i] & qand) ^ qxor;
-      qreg[s] = as_bf16x8(v);
+      for (int s = 0; s < C::KSD; ++s) {
+        u32x4 v = as_u32x4(qreg[s]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = (v[i] & qand) ^ qxor;
+        qreg[s] = as_bf16x8(v);
+      }
     }
     if constexpr (C::KSR > 0) {
       const uint32_t rrb = (uint32_t)P.rq.ss * 2u;
