@@ -139,6 +139,27 @@ def test_varlen_random_shapes_d64(gpu, seed):
     _varlen_case(gpu, lengths, Hq, 64, H_KV, H_G, R, causal, seed=seed)
 
 
+@pytest.mark.parametrize("seed", [217, 201, 207, 223, 200, 237, 214, 242, 227, 206])
+def test_varlen_random_shapes_d128(gpu, seed):
+    """Seeded random packs at d 128 (the forward and dQ read their LDS
+    operands k-steps ahead of the MFMAs there, in chains whose length
+    depends on the rank tier): every rank from 8 to 64, lengths with the
+    32 / 128-key tile edges over-represented, GQA groups of 1 to 3 with any
+    number of graph heads, causal or not (the seeds cover ranks 8 to 64,
+    each rank tier causal and not)."""
+    rng = np.random.default_rng(seed)
+    edges = [1, 31, 32, 33, 63, 64, 65, 127, 128, 129, 160, 257]
+    n = int(rng.integers(2, 7))
+    lengths = [int(rng.choice(edges)) if rng.random() < 0.5 else int(rng.integers(1, 450))
+               for _ in range(n)]
+    H_KV = int(rng.integers(1, 3))
+    Hq = H_KV * int(rng.integers(1, 4))
+    H_G = int(rng.integers(0, Hq + 1))
+    R = 8 * int(rng.integers(1, 9)) if H_G else 0
+    causal = bool(rng.integers(0, 2))
+    _varlen_case(gpu, lengths, Hq, 128, H_KV, H_G, R, causal, seed=seed)
+
+
 def test_varlen_d64_rank_rows_past_20k(gpu):
     """d 64, 8 graph heads of rank 32: a tile's rank rows past 20 KB.  Caught a
     missing wait state between a scalar descriptor write and the inline-asm
