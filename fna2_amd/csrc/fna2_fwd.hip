@@ -40,10 +40,11 @@ struct FwdCfg {
   static constexpr int RBYTES = BN * RPL * 2;
   static constexpr int VBYTES = BN * D * 2;
   static constexpr int STAGE = KBYTES + RBYTES + VBYTES;
-  // d = 128, rank tile <= 32: K operand reads in flight ahead of the S
-  // MFMAs and V^T operands ahead of the O MFMAs (the register budget of
-  // three waves per SIMD leaves room for two each; none at rank 64).
-  static constexpr bool PIPE = D == 128 && RPL <= 32;
+  // Rank tile <= 32: K operand reads in flight ahead of the S MFMAs and
+  // V^T operands ahead of the O MFMAs (the register budget of three waves
+  // per SIMD at d = 128, four at d = 64, leaves room for two each; none at
+  // rank 64).
+  static constexpr bool PIPE = RPL <= 32;
   static constexpr int kAhead = 2;
   static constexpr int kAhead2 = 2;
 };
@@ -85,12 +86,11 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
   const int kvh = h / p.group;
   const bool graph = (RPL > 0) && (h < p.H_G);
   const float bh = uni_f(graph ? *const_space(P.gs + h) / p.c : 0.f);
-  const int nrs = graph ? (S16 ? 2 : cdiv(p.R, 16)) : 0;  // rank steps actually used
-  // d = 128: the rank MFMAs run unconditionally (rank features past R and a
-  // vanilla head's rank operands are zeros on both sides).  A branch around
-  // them made the compiler zero the accumulator registers before it; at
-  // d = 64 the branch measured faster all the same (c2), and stays.
-  constexpr bool RANK_ALL = D == 128;
+  // The rank MFMAs run unconditionally: rank features past R and a vanilla
+  // head's rank operands are zeros on both sides (its rank tiles are DMA'd
+  // from a zero-size range).  A branch around them made the compiler zero
+  // the accumulator registers before it (at d = 128 c4 forward -2%; at
+  // d = 64, with the operand reads ahead, c5 forward -2%).
 
   const uint16_t* qb = seq_base<const uint16_t>(P.q, p, b, e.q0, h);
   const uint16_t* kb = seq_base<const uint16_t>(P.k, p, b, e.k0, kvh);
@@ -125,11 +125,10 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
     const uint32_t rows = (uint32_t)max(min(C::BN, e.lk - k0), 0);
     dk.issue(make_rsrc(kb + (int64_t)k0 * P.k.ss, rows * krb), base, wv);
     if constexpr (C::CR > 0) {
-      // (RANK_ALL: a vanilla head's rank tile is a zero-size range, so the
-      // DMA writes zeros and its rank MFMAs add exact zeros)
-      if (RANK_ALL || graph)
-        dr.issue(make_rsrc(rkb + (int64_t)k0 * P.rk.ss, graph ? rows * rkrb : 0u),
-                 base + C::KBYTES, wv);
+      // (a vanilla head's rank tile is a zero-size range: the DMA writes
+      // zeros and its rank MFMAs add exact zeros)
+      dr.issue(make_rsrc(rkb + (int64_t)k0 * P.rk.ss, graph ? rows * rkrb : 0u), base + C::KBYTES,
+               wv);
     }
     dv.issue(make_rsrc(vb + (int64_t)k0 * P.v.ss, rows * vrb), base + C::KBYTES + C::RBYTES, wv);
   };
@@ -228,8 +227,7 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
       if constexpr (C::KSR > 0) {
 #pragma unroll
         for (int s = 0; s < C::KSR; ++s)
-          if (RANK_ALL || s < nrs)
-            acc = mfma32(row_read<C::BN>(rl, rdl, kb2 * 32, s), qreg[C::KSD + s], acc);
+          acc = mfma32(row_read<C::BN>(rl, rdl, kb2 * 32, s), qreg[C::KSD + s], acc);
         if constexpr (!S16) acc *= here_s(bh);
       }
       if constexpr (C::PIPE) {
