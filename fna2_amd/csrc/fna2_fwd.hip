@@ -40,13 +40,13 @@ struct FwdCfg {
   static constexpr int RBYTES = BN * RPL * 2;
   static constexpr int VBYTES = BN * D * 2;
   static constexpr int STAGE = KBYTES + RBYTES + VBYTES;
-  // Rank tile <= 32: K operand reads in flight ahead of the S MFMAs and
-  // V^T operands ahead of the O MFMAs (the register budget of three waves
-  // per SIMD at d = 128, four at d = 64, leaves room for two each; none at
-  // rank 64).
+  // Rank tile <= 32: K operand reads in flight kAhead k-steps ahead of the
+  // S MFMAs (the register budget of three waves per SIMD at d = 128, four
+  // at d = 64, leaves room for two; none at rank 64).  V^T operands
+  // kAhead2 MFMAs ahead of the O MFMAs: two, one at rank 64.
   static constexpr bool PIPE = RPL <= 32;
   static constexpr int kAhead = 2;
-  static constexpr int kAhead2 = 2;
+  static constexpr int kAhead2 = PIPE ? 2 : 1;
 };
 
 // S16 (R <= 16, rank tile 32): the rank chain accumulates b <Rq, Rk>
@@ -281,25 +281,27 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
     const float nm = -((m_i == kNegInf) ? 0.f : m_i) * p.c2;
     float ls = 0.f;
     bf16x8 pb[C::BN / 16];
+    u32x4 pk[C::BN / 16];
+    // pairs i0 .. i1 - 1 of P operand q (16 keys: accumulator kb2 = q / 2,
+    // registers 8 (q % 2) .. +7)
+    auto exps = [&](int q, int i0, int i1) {
 #pragma unroll
-    for (int kb2 = 0; kb2 < C::BN / 32; ++kb2)
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        u32x4 pk;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int v0 = 8 * half + 2 * i;
-          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb2][v0], p.c2, nm));
-          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kb2][v0 + 1], p.c2, nm));
-          ls += p0 + p1;
-          pk[i] = pack_e<F16>(p0, p1);
-        }
-        pb[kb2 * 2 + half] = as_bf16x8(pk);
+      for (int i = i0; i < i1; ++i) {
+        const int v0 = 8 * (q & 1) + 2 * i;
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[q >> 1][v0], p.c2, nm));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[q >> 1][v0 + 1], p.c2, nm));
+        ls += p0 + p1;
+        pk[q][i] = pack_e<F16>(p0, p1);
       }
-    l_i += ls;
-    // O^T += V^T P^T
-    if constexpr (C::PIPE) {
-      constexpr int A = C::kAhead2, N = (C::BN / 16) * (D / 32);
+      if (i1 == 4) pb[q] = as_bf16x8(pk[q]);
+    };
+    // O^T += V^T P^T, with the exponentials of P operand s + 1 between the
+    // MFMAs of operand s, where they hide the MFMAs' operand reads (c5
+    // forward -1.3%; at rank 64, where the compiler read each operand just
+    // before its MFMA, c4 -1.1% with the reads one MFMA ahead)
+    {
+      constexpr int A = C::kAhead2, NS = C::BN / 16, N = NS * (D / 32), PPM = 4 / (D / 32);
+      exps(0, 0, 4);
       bf16x8 vr[A];
 #pragma unroll
       for (int i = 0; i < A; ++i) vr[i] = tr_operand<C::BN>(vl, tl, 16 * (i / (D / 32)), 32 * (i % (D / 32)));
@@ -311,13 +313,10 @@ __device__ __forceinline__ void fwd_body(const FwdParams& P) {
         if (i + A < N)
           vr[i % A] = tr_operand<C::BN>(vl, tl, 16 * ((i + A) / (D / 32)), 32 * ((i + A) % (D / 32)));
         __builtin_amdgcn_sched_barrier(0);
+        if (s + 1 < NS) exps(s + 1, PPM * d, PPM * d + PPM);
+        __builtin_amdgcn_sched_barrier(0);
       }
-    } else {
-#pragma unroll
-      for (int s = 0; s < C::BN / 16; ++s)
-#pragma unroll
-        for (int d = 0; d < D / 32; ++d)
-          oacc[d] = mfma_e<F16>(tr_operand<C::BN>(vl, tl, 16 * s, 32 * d), pb[s], oacc[d]);
+      l_i += ls;
     }
   };
 
