@@ -96,10 +96,12 @@ struct KvCfg {
   // The ring tiles of a block: Q, the rank operand, dO and the -LSE log2(e)
   // / delta rows.  CDMA: those the consumer waves DMA (at the start of their
   // step); the producers DMA the rest (at the end of theirs).  With two key
-  // slices per wave the consumers have the time for all of them; with one
-  // their own step is the longer with any (measured), and the producers
-  // keep them.
-  static constexpr unsigned CDMA = KPW == 2 ? kTileAll : 0u;
+  // slices per wave the consumers have the time for all of them.  With one,
+  // at d = 128 and rank 64 (no K | Rk tiles for them to DMA) they take the
+  // dO tile (c4 dK/dV -3%; the -LSE / delta rows as well: +4.5%); at rank
+  // 32 their own step is the longer with any (c3 +2 to +4 us), and the
+  // producers keep them.
+  static constexpr unsigned CDMA = KPW == 2 ? kTileAll : (D == 128 && RPL == 64) ? kTileO : 0u;
   // VMEM instructions per wave and block for the tiles in mask m.
   static constexpr int nb_of(unsigned m) {
     return ((m & kTileQ) ? DmaD::PER_WAVE : 0) +
