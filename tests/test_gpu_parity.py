@@ -168,6 +168,16 @@ def test_varlen_d64_rank_rows_past_20k(gpu):
     _varlen_case(gpu, [300], 8, 64, 8, 8, 32, False, seed=23)
 
 
+@pytest.mark.parametrize("D,R", [(64, 48), (64, 16), (128, 64)])
+def test_vanilla_heads_with_rank_tiles(gpu, D, R):
+    """Vanilla heads next to graph heads in every kernel variant whose rank
+    MFMAs run for all heads: the vanilla heads' rank tiles come from
+    zero-size ranges, so their scores must equal plain attention's."""
+    _dense_case(gpu, 2, 4, 160, D, 2, 2, R, True, seed=D + R + 1)
+    _varlen_case(gpu, [300, 17, 129, 64], 4, D, 2, 1, R, False, seed=D + R + 2)
+    _varlen_case(gpu, [95, 1, 256], 6, D, 3, 4, R, True, seed=D + R + 3)
+
+
 def test_varlen_cross_lengths(gpu):
     lq = [50, 130, 7, 200]
     lk = [70, 100, 7, 260]
