@@ -913,8 +913,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build runs the "
-              "kernels on a single MI355X; multi-GPU sharding is described in DESIGN.md and "
-              "is not run.", file=sys.stderr)
+              "kernels on a single MI355X; sharding over several GPUs is not built.",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
