@@ -850,8 +850,9 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
         // A transposed operands are read, then each MFMA pair's operand is
         // read A operands ahead, behind scheduling fences (the compiler's
         // own order, group barriers notwithstanding, waited for 9 of the 20
-        // reads just issued: c2 dK/dV 115.6 -> 112.6 us, c5 421 -> 413).
-        constexpr int NO = 2 * C::NDB + C::NRB, A = 2;
+        // reads just issued: c2 dK/dV 115.6 -> 112.6 us, c5 421 -> 413;
+        // three ahead instead of two: c2 -1.9%, c5 -0.5%; four: no better).
+        constexpr int NO = 2 * C::NDB + C::NRB, A = 3;
         auto opnd = [&](int j, int r) {
           return r < C::NDB ? tr_operand<C::BM>(ot, tl, 16 * j, 32 * r)
                  : r < 2 * C::NDB ? tr_operand<C::BM>(qt, tl, 16 * j, 32 * (r - C::NDB))
