@@ -424,8 +424,8 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
     // this wave's key slices against block qi of the cursor.
     // The block's -LSE log2(e) and delta rows go to lsr (this lane's query
     // rows 8 gq + 4 hl .. +3, gq = 0..3: -LSE in lsr[gq], delta in
-    // lsr[4 + gq]), read with the operands so their latency hides under the
-    // MFMAs.
+    // lsr[4 + gq]), read after the rank MFMAs so that their latency hides
+    // under the S chain.
     auto scores = [&](const KvCursor& c, const uint8_t* cur, f32x16 (&sacc)[C::KPW],
                       f32x16 (&dpacc)[C::KPW], f32x4_t (&lsr)[8]) {
       // (A vanilla head, or rank padding, has zero rank operands: its rank
@@ -470,14 +470,13 @@ __device__ __forceinline__ void dkdv_body(const BwdParams& P) {
 #pragma unroll
         for (int j = 0; j < C::KPW; ++j)
           sacc[j] = mfma_e<F16>(qa[s], as_bf16x8(kreg[j][s]), sacc[j]);
-      // issue order: every read, then the rank MFMAs, then (after the
-      // scaling) the head-dim MFMAs of S (with two key slices the -LSE /
-      // delta reads between the two, so that those registers are not live
-      // with all the operands).
-      constexpr int LSR_FIRST = C::KPW == 1 ? 8 : 0;
-      __builtin_amdgcn_sched_group_barrier(0x100, 2 * C::KSD + C::KSR + LSR_FIRST, 0);
+      // issue order: the operand reads, the rank MFMAs, the -LSE / delta
+      // reads, then (after the scaling) the head-dim MFMAs of S.  (The -LSE
+      // / delta reads with the operands instead: c2 / c5 dK/dV +2% with two
+      // key slices, c3 +1.4 us and c4 +0.6% with one.)
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * C::KSD + C::KSR, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, C::KSR * C::KPW, 0);
-      if constexpr (LSR_FIRST == 0) __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, C::KSD * C::KPW, 0);
       __builtin_amdgcn_sched_barrier(0);
       // The dP chain, and between its MFMAs the exponentials of the finished
